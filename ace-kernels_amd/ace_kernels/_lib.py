@@ -1,0 +1,96 @@
+"""ctypes binding of ``libace_hip.so`` (the C-ABI declared in ``include/ace_hip.h``).
+
+The library is the only implementation of the loss in this package: if it is
+missing or fails to load, every call raises -- there is no fallback path.
+Build it with ``python ace-kernels_amd/build.py``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from functools import lru_cache
+from pathlib import Path
+
+LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
+
+ABI_VERSION = 1
+
+# enums of include/ace_hip.h
+F32, BF16, F16 = 0, 1, 2
+TARGET_LABELS_I64, TARGET_ONEHOT_F32 = 0, 1
+HARD, SOFT = 0, 1
+ACT_NONE, ACT_SOFTMAX, ACT_SIGMOID = 0, 1, 2
+RED_MEAN, RED_SUM, RED_NONE = 0, 1, 2
+
+# every symbol include/ace_hip.h declares
+EXPORTS = (
+    "ace_abi_version",
+    "ace_error_string",
+    "ace_workspace_bytes",
+    "ace_workspace_reset_bytes",
+    "ace_forward",
+    "ace_backward",
+)
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+
+class AceLibraryError(RuntimeError):
+    """libace_hip.so is missing, stale, or returned an error code."""
+
+
+@lru_cache(maxsize=1)
+def lib() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise AceLibraryError(
+            f"{LIB_PATH} not found: the HIP extension is not built "
+            "(run `python ace-kernels_amd/build.py`)"
+        )
+    # the process's HIP runtime is torch's; load it first so the library binds to it
+    import torch  # noqa: F401
+
+    handle = ctypes.CDLL(str(LIB_PATH))
+    handle.ace_abi_version.restype = _i
+    handle.ace_abi_version.argtypes = []
+    handle.ace_error_string.restype = ctypes.c_char_p
+    handle.ace_error_string.argtypes = [_i]
+    for name in ("ace_workspace_bytes", "ace_workspace_reset_bytes"):
+        fn = getattr(handle, name)
+        fn.restype = _sz
+        fn.argtypes = [_i64, _i64, _i64, _i, _i, _i, _i]
+    handle.ace_forward.restype = _i
+    handle.ace_forward.argtypes = [
+        _p, _i, _p, _i,            # x, dtype, target, kind
+        _i64, _i64, _i64,          # B, C, N
+        _i, _i, _i,                # K, binning, activation
+        _i, _i, _i, _i,            # include_bg, ignore_empty, reduction, right
+        _f, _p, _p, _p,            # empty_weight, class_weight, bin_table, centre_table
+        _p, _sz,                   # workspace, bytes
+        _p, _p, _p, _p, _p, _p,    # coef, diff, jac, per_class, loss, stats
+        _p,                        # stream
+    ]
+    handle.ace_backward.restype = _i
+    handle.ace_backward.argtypes = [
+        _p, _i, _p, _i,
+        _i64, _i64, _i64,
+        _i, _i, _i, _i, _i,        # K, binning, activation, include_bg, right
+        _p, _p,                    # bin_table, centre_table
+        _p, _p, _p,                # coef, diff, jac
+        _p, _i,                    # grad_output, per_class
+        _p, _p,                    # dx, stream
+    ]
+    version = handle.ace_abi_version()
+    if version != ABI_VERSION:
+        raise AceLibraryError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}: rebuild it")
+    return handle
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().ace_error_string(rc).decode()
+        raise AceLibraryError(f"{what} failed with code {rc}: {msg}")

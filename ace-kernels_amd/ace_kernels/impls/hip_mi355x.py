@@ -1,0 +1,206 @@
+"""The MI355X implementation: ``torch.autograd.Function`` over the HIP C-ABI.
+
+Mirrors the reference's fastest implementation, ``_V6Loss``
+(``src/ace_kernels/impls/v6_triton.py:93-111``, with ``_forward`` ``:43-65``
+and ``_backward`` ``:68-90``): logits in (float32 / bfloat16 / float16),
+d logits out in the logits' dtype; saved for backward are the inputs
+(already held by the caller) plus ``coef``, ``d`` ``[B, C', K]`` and ``jac``
+``[B, C']``.  The forward is one kernel launch (histograms, cross-block
+reduction and epilogue); the backward is one launch.
+
+Input handling follows ``as_kernel_input`` (``kernels/act.py:69-73``) and
+``_kernel_target`` (``impls/v5_triton.py:25-32``): logits are viewed as
+``[B, C, N]``; with ``to_onehot_y`` and C > 1 the target is read as ``[B, N]``
+int64 class indices (one-hot conversion fused into the kernels), else as
+``[B, C, N]`` float32 targets.  Errors mirror the reference: a bad input rank
+raises ``ValueError`` (``common.py:104-105``), a target/input shape mismatch
+``AssertionError`` (``common.py:117-118``), bad class weights ``ValueError``.
+
+float64 input is rejected with ``TypeError``: every kernel computes in
+float32 (the reference's GPU path falls back to a PyTorch implementation for
+float64, ``v6_triton.py:226-227``; this package has no non-HIP path).
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional, Tuple
+
+import torch
+
+from ace_kernels import _lib
+from ace_kernels.common import bin_tables, class_weight_tensor, class_weights, workspace
+from ace_kernels.config import ACEConfig
+from ace_kernels.registry import register
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+_REDUCTIONS = {"mean": _lib.RED_MEAN, "sum": _lib.RED_SUM, "none": _lib.RED_NONE}
+
+
+class Plan:
+    """Kernel-ready views of one call's inputs plus the scalar arguments."""
+
+    __slots__ = (
+        "x", "dtype_code", "target", "target_kind", "B", "C", "N", "CL", "K",
+        "soft", "act", "include_bg", "right", "spatial_ndim", "in_shape",
+        "btab", "rtab",
+    )
+
+
+def _activation_code(config: ACEConfig, channels: int) -> int:
+    """Softmax over one channel is the identity, as in the reference."""
+    if config.activation == "sigmoid":
+        return _lib.ACT_SIGMOID
+    if config.activation == "softmax" and channels > 1:
+        return _lib.ACT_SOFTMAX
+    return _lib.ACT_NONE
+
+
+def make_plan(input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> Plan:
+    if input.dim() < 3:
+        raise ValueError(f"input must be [B, C, *spatial], got {tuple(input.shape)}")
+    if input.device.type != "cuda":
+        raise ValueError(f"hip_mi355x needs a HIP ('cuda') tensor, got {input.device}")
+    if input.dtype == torch.float64:
+        raise TypeError("hip_mi355x computes in float32: float64 input is not supported")
+    code = _DTYPES.get(input.dtype)
+    x = input if code is not None else input.float()
+    code = _DTYPES[x.dtype]
+    b, c = x.shape[:2]
+    x = x.reshape(b, c, -1)
+    if not x.is_contiguous():
+        x = x.contiguous()
+    n = x.shape[2]
+    pl = Plan()
+    pl.x, pl.dtype_code = x, code
+    pl.B, pl.C, pl.N = int(b), int(c), int(n)
+    pl.include_bg = bool(config.include_background or c == 1)
+    pl.CL = pl.C - (0 if pl.include_bg else 1)
+    pl.K = int(config.num_bins)
+    pl.soft = config.binning == "soft"
+    pl.act = _activation_code(config, c)
+    pl.right = bool(config.right)
+    pl.spatial_ndim = input.dim() - 2
+    pl.in_shape = input.shape
+    if target.device != input.device:
+        raise ValueError(f"target is on {target.device}, input on {input.device}")
+    if config.to_onehot_y and c > 1:
+        t = target.reshape(b, -1)
+        if t.shape[1] != n:
+            raise AssertionError("target and input spatial sizes differ")
+        if t.dtype != torch.int64:
+            t = t.long()
+        pl.target, pl.target_kind = t.contiguous(), _lib.TARGET_LABELS_I64
+    else:
+        if target.numel() != b * c * n:
+            raise AssertionError(
+                f"ground truth has different shape ({tuple(target.shape)}) from input "
+                f"({tuple(input.shape)})"
+            )
+        t = target.reshape(b, c, n)
+        if t.dtype != torch.float32:
+            t = t.float()
+        pl.target, pl.target_kind = t.contiguous(), _lib.TARGET_ONEHOT_F32
+    pl.btab, pl.rtab = bin_tables(pl.K, pl.soft, x.device)
+    return pl
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False):
+    """(loss, coef, d, jac, per_class, stats-or-None) via ``ace_forward``."""
+    lib = _lib.lib()
+    dev = pl.x.device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    binning = _lib.SOFT if pl.soft else _lib.HARD
+    ws_bytes = lib.ace_workspace_bytes(pl.B, pl.C, pl.N, pl.K, binning, pl.dtype_code, int(pl.include_bg))
+    ws = workspace(dev, stream, ws_bytes)
+    f32 = torch.float32
+    coef = torch.empty((pl.B, pl.CL, pl.K), dtype=f32, device=dev)
+    d = torch.empty_like(coef)
+    jac = torch.empty((pl.B, pl.CL), dtype=f32, device=dev)
+    per_class = torch.empty_like(jac)
+    reduction = _REDUCTIONS[config.reduction]
+    loss = torch.empty((), dtype=f32, device=dev) if reduction != _lib.RED_NONE else None
+    st = torch.empty((3, pl.B, pl.CL, pl.K), dtype=torch.float64, device=dev) if stats else None
+    weights = class_weights(config, pl.CL)
+    cw = class_weight_tensor(tuple(weights), dev) if weights is not None else None
+    rc = lib.ace_forward(
+        pl.x.data_ptr(), pl.dtype_code, pl.target.data_ptr(), pl.target_kind,
+        pl.B, pl.C, pl.N, pl.K, binning, pl.act,
+        int(pl.include_bg), int(config.ignore_empty_classes), reduction, int(pl.right),
+        float(config.empty_weight), _ptr(cw), pl.btab.data_ptr(), _ptr(pl.rtab),
+        ws.data_ptr(), ws.numel(),
+        coef.data_ptr(), d.data_ptr(), jac.data_ptr(), per_class.data_ptr(), _ptr(loss), _ptr(st),
+        stream,
+    )
+    _lib.check(rc, "ace_forward")
+    if loss is None:
+        loss = per_class.view(pl.B, pl.CL, *([1] * pl.spatial_ndim))
+    return loss, coef, d, jac, per_class, st
+
+
+def hip_backward(pl: Plan, coef: torch.Tensor, d: torch.Tensor, jac: torch.Tensor,
+                 grad_output: torch.Tensor) -> torch.Tensor:
+    """d loss / d input (input's shape and dtype) via ``ace_backward``."""
+    lib = _lib.lib()
+    dev = pl.x.device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    per_class = grad_output.dim() > 0
+    go = grad_output
+    if go.dtype != torch.float32:
+        go = go.float()
+    go = go.reshape(-1) if per_class else go.reshape(())
+    if not go.is_contiguous():
+        go = go.contiguous()
+    dx = torch.empty_like(pl.x)
+    rc = lib.ace_backward(
+        pl.x.data_ptr(), pl.dtype_code,
+        pl.target.data_ptr() if pl.soft else None, pl.target_kind,
+        pl.B, pl.C, pl.N, pl.K, _lib.SOFT if pl.soft else _lib.HARD, pl.act,
+        int(pl.include_bg), int(pl.right),
+        pl.btab.data_ptr(), _ptr(pl.rtab),
+        coef.data_ptr(), d.data_ptr(), jac.data_ptr(),
+        go.data_ptr(), int(per_class),
+        dx.data_ptr(), stream,
+    )
+    _lib.check(rc, "ace_backward")
+    return dx.view(pl.in_shape)
+
+
+class _HipACELoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> torch.Tensor:
+        pl = make_plan(input, target, config)
+        loss, coef, d, jac, _, _ = hip_forward(pl, config)
+        # the kernel views of input / target go through save_for_backward (same
+        # storage as the caller's tensors; version-checked by autograd)
+        ctx.save_for_backward(pl.x, pl.target, coef, d, jac)
+        pl.x = pl.target = None
+        ctx.plan = pl
+        return loss
+
+    @staticmethod
+    def backward(ctx: Any, grad_output: torch.Tensor) -> Tuple[Optional[torch.Tensor], None, None]:
+        x, target, coef, d, jac = ctx.saved_tensors
+        pl = ctx.plan
+        pl.x, pl.target = x, target
+        try:
+            dx = hip_backward(pl, coef, d, jac, grad_output)
+        finally:
+            pl.x = pl.target = None
+        return dx, None, None
+
+
+def hip_ace(input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> torch.Tensor:
+    """Registry entry ``fn(input, target, config) -> loss``."""
+    loss: torch.Tensor = _HipACELoss.apply(input, target, config)
+    return loss
+
+
+register(
+    "hip_mi355x",
+    description="MI355X HIP kernels: fused softmax/binning/histogram forward, one-pass backward",
+    devices=frozenset({"cuda"}),
+)(hip_ace)

@@ -1,0 +1,101 @@
+"""Build libace_hip.so (the C-ABI of the HIP kernels) for gfx950 with hipcc.
+
+    python ace-kernels_amd/build.py            # compile + link
+    python ace-kernels_amd/build.py --check    # also print kernel resource usage
+
+Each translation unit under csrc/ is compiled to an object in parallel, then
+linked into ace_kernels/libace_hip.so, next to the Python package that loads
+it.  Every HIP compile line carries
+``-Xclang -target-feature -Xclang -packed-fp32-ops`` (no packed fp32 VALU) and
+``-ffp-contract=off`` (no implicit FMA contraction: the probabilities and bin
+weights must be rounded exactly as written).
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent
+CSRC = HERE / "csrc"
+INCLUDE = ROOT / "include"
+OUT_DIR = HERE / "ace_kernels"
+LIB = OUT_DIR / "libace_hip.so"
+OBJ_DIR = HERE / "_build"
+
+ARCH = os.environ.get("ACE_OFFLOAD_ARCH", "gfx950")
+
+HIP_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-ffp-contract=off",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm under /opt/rocm)")
+
+
+def _compile(src: Path, extra: list) -> Path:
+    obj = OBJ_DIR / (src.stem + ".o")
+    cmd = [hipcc(), *HIP_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = False, extra: list | None = None) -> Path:
+    """Compile every csrc/*.hip and link ace_kernels/libace_hip.so; return its path."""
+    extra = list(extra or [])
+    OBJ_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, extra), sources))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB} from {len(sources)} sources")
+    return LIB
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--check", action="store_true", help="print register/LDS usage (-Rpass-analysis)")
+    args = ap.parse_args()
+    extra = ["-Rpass-analysis=kernel-resource-usage"] if args.check else []
+    if args.check:
+        OBJ_DIR.mkdir(exist_ok=True)
+        for src in sorted(CSRC.glob("*.hip")):
+            cmd = [hipcc(), *HIP_FLAGS, *extra, "-c", str(src), "-o", str(OBJ_DIR / (src.stem + ".o"))]
+            res = subprocess.run(cmd, capture_output=True, text=True)
+            sys.stdout.write(res.stderr)
+    build(verbose=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

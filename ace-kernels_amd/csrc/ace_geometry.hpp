@@ -1,0 +1,121 @@
+// Launch geometry and device-memory layout shared by the host dispatch and the
+// kernels.  Host-only arithmetic; no HIP calls.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ace {
+
+constexpr int kThreads = 256;           // threads per block (4 wave64)
+constexpr int kFrac = 30;               // fixed-point fraction bits of the sums
+constexpr int kMaxChannels = 64;        // largest C with a built kernel
+constexpr size_t kMaxHistLds = 64 * 1024;  // LDS budget of the histogram copies
+
+// Channel variants with a compiled kernel: the kernel keeps C logits of VEC
+// voxels in registers.  EXACT variants fix C at compile time; the others
+// handle any C up to CMAX with uniform guards.
+struct Variant {
+  int cmax;
+  bool exact;
+  int vec;  // voxels per thread and step
+};
+
+inline Variant variant_for(int64_t C) {
+  if (C == 1) return {1, true, 4};
+  if (C == 2) return {2, true, 4};
+  if (C == 3) return {3, true, 4};
+  if (C == 4) return {4, true, 4};
+  if (C <= 8) return {8, false, 4};
+  if (C == 16) return {16, true, 4};
+  if (C <= 16) return {16, false, 4};
+  if (C <= 32) return {32, false, 1};
+  return {64, false, 1};
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Bytes of one histogram copy for a (C' * K)-bin block histogram.
+//   hard: u64 packed (count << 48 | sum p) + G (u32 count for labels,
+//         i64 fixed-point for per-channel targets)
+//   soft: three i64 fixed-point sums W, P, G
+constexpr size_t hist_bytes_per_copy(int ck, bool soft, bool labels) {
+  return soft ? (size_t)ck * 24 : (size_t)ck * (labels ? 12 : 16);
+}
+
+struct Geometry {
+  Variant var;
+  int C, CL, off, K, ck;
+  int64_t B, N;
+  int steps;           // vector steps per block
+  int64_t tile_vox;    // voxels per block (one batch index)
+  int64_t tiles;       // blocks per batch index
+  int64_t nblk;        // total blocks
+  int64_t gs;          // blocks per reduction group
+  int64_t gpb;         // groups per batch index
+  int copies;          // histogram copies (lane % copies)
+  size_t tab_floats;   // padded bucket table (n + 2) + centre table (2K + 2)
+  size_t lds_fwd;      // dynamic LDS of the forward kernel
+  size_t lds_bwd;      // dynamic LDS of the backward kernel
+  size_t ws_counters;  // bytes of ticket counters (must start zeroed)
+  size_t off_part, off_gpart, ws_bytes;
+};
+
+// Blocks per batch index: aim for ~8 blocks per CU on a 256-CU part while
+// keeping every block's tile a whole number of vector steps.
+inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
+                              bool soft, bool include_background, bool labels,
+                              int steps_override = 0) {
+  Geometry g{};
+  g.var = variant_for(C);
+  g.C = (int)C;
+  g.off = (!include_background && C > 1) ? 1 : 0;
+  g.CL = (int)C - g.off;
+  g.K = K;
+  g.ck = g.CL * K;
+  g.B = B;
+  g.N = N;
+  const int64_t step_vox = (int64_t)kThreads * g.var.vec;
+  int steps = steps_override;
+  if (steps <= 0) {
+    const int64_t total = B * (N > 0 ? N : 1);
+    const int64_t target_blocks = 2048;
+    steps = (int)cdiv(total, step_vox * target_blocks);
+    if (steps < 1) steps = 1;
+    if (steps > 64) steps = 64;
+  }
+  g.steps = steps;
+  g.tile_vox = step_vox * steps;
+  g.tiles = N > 0 ? cdiv(N, g.tile_vox) : 1;
+  g.nblk = B * g.tiles;
+  // two-level reduction: groups of ~sqrt(tiles) blocks
+  int64_t gs = 1;
+  while (gs * gs < g.tiles) ++gs;
+  if (gs > 64) gs = 64;
+  g.gs = gs;
+  g.gpb = cdiv(g.tiles, gs);
+  const size_t per_copy = hist_bytes_per_copy(g.ck, soft, labels);
+  int copies = 16;
+  while (copies > 1 && per_copy * copies > kMaxHistLds) copies /= 2;
+  g.copies = copies;
+  const int n = soft ? 2 * K : K;
+  g.tab_floats = align_up((size_t)(n + 2) + (soft ? (size_t)(2 * K + 2) : 0), 4);
+  // the last block reuses the histogram region for the epilogue:
+  // d, W, G, per-class f (float) and an empty flag per bin of one batch index
+  const size_t epi = align_up((size_t)g.ck * 17, 16);
+  const size_t hist = align_up(per_copy * copies, 16);
+  g.lds_fwd = g.tab_floats * 4 + (hist > epi ? hist : epi);
+  // backward: tables + coef (+ d) + g
+  g.lds_bwd = g.tab_floats * 4 + align_up((size_t)g.ck * (soft ? 2 : 1) + g.CL, 4) * 4;
+  const int64_t counters = B * g.gpb + 1;
+  g.ws_counters = align_up((size_t)counters * sizeof(int), 256);
+  const size_t part_bytes = (size_t)g.nblk * 3 * g.ck * sizeof(long long);
+  const size_t gpart_bytes = (size_t)(B * g.gpb) * 3 * g.ck * sizeof(long long);
+  g.off_part = g.ws_counters;
+  g.off_gpart = align_up(g.off_part + part_bytes, 256);
+  g.ws_bytes = align_up(g.off_gpart + gpart_bytes, 256);
+  return g;
+}
+
+}  // namespace ace

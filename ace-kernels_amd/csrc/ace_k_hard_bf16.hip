@@ -1,0 +1,6 @@
+// Kernel instantiations: hard binning, __hip_bfloat16 logits.
+#include "ace_core.hpp"
+
+namespace ace {
+ACE_DEFINE_LAUNCHERS(__hip_bfloat16, false)
+}  // namespace ace

@@ -1,0 +1,128 @@
+/*
+ * ace_hip.h -- C-ABI of the MI355X (gfx950) mL1-ACE loss hot path.
+ *
+ * Two entry points replace the reference's GPU path:
+ *
+ *   ace_forward  replaces the forward of the reference's fastest impl,
+ *                `_forward` in src/ace_kernels/impls/v6_triton.py:43-65, i.e.
+ *                the fused histogram kernels `hard_hist_fused`
+ *                (src/ace_kernels/kernels/hard_hist.py:186-233) /
+ *                `soft_hist_fused` (kernels/soft_hist.py:229-271) followed by
+ *                `epilogue_triton` (kernels/epilogue.py:93-129).
+ *   ace_backward replaces `_backward` (impls/v6_triton.py:68-90), i.e.
+ *                `hard_input_grad_triton` (kernels/hard_bwd.py:98-149) /
+ *                `soft_input_grad_triton` (kernels/soft_bwd.py:102-163) with
+ *                g = jac * grad_output fused in.
+ *
+ * Conventions
+ *   - All pointers except `class_weight == NULL`, `stats == NULL` and the
+ *     host-only arguments are device pointers on the current HIP device.
+ *   - `stream` is a hipStream_t (0 = the null stream).  Every launch is
+ *     asynchronous on it; no call synchronises, copies host<->device or
+ *     allocates device memory, so both calls can be captured in a HIP graph.
+ *   - Logits `x` are [B, C, N] contiguous (channels-first, N = prod(spatial)).
+ *   - Targets are either class indices [B, N] (int64, original class
+ *     numbering, ACE_TARGET_LABELS_I64) or per-channel targets [B, C, N]
+ *     (float32, ACE_TARGET_ONEHOT_F32).
+ *   - C' = C - 1 when include_background == 0 and C > 1, else C.
+ *   - Return value: 0 on success, otherwise an ACE_E* code (see
+ *     ace_error_string); a HIP launch failure returns ACE_EHIP + hipError_t.
+ */
+#ifndef ACE_HIP_H
+#define ACE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element type of x (and of dx) */
+enum { ACE_F32 = 0, ACE_BF16 = 1, ACE_F16 = 2 };
+/* target layout */
+enum { ACE_TARGET_LABELS_I64 = 0, ACE_TARGET_ONEHOT_F32 = 1 };
+/* binning (ACEConfig.binning) */
+enum { ACE_HARD = 0, ACE_SOFT = 1 };
+/* activation applied in-kernel; softmax over C == 1 must be passed as NONE */
+enum { ACE_ACT_NONE = 0, ACE_ACT_SOFTMAX = 1, ACE_ACT_SIGMOID = 2 };
+/* reduction over the [B, C'] per-class errors */
+enum { ACE_RED_MEAN = 0, ACE_RED_SUM = 1, ACE_RED_NONE = 2 };
+
+/* error codes */
+enum {
+  ACE_OK = 0,
+  ACE_EINVAL = 1,       /* bad argument (null pointer, size, enum value)     */
+  ACE_EUNSUPPORTED = 2, /* valid but not built: e.g. C > 64, LDS too large    */
+  ACE_EWORKSPACE = 3,   /* workspace smaller than ace_workspace_bytes()       */
+  ACE_EHIP = 1000       /* + hipError_t of a failed launch                    */
+};
+
+/* ABI version of this header (incremented on any signature change). */
+int ace_abi_version(void);
+
+/* Human-readable text for a return code (static storage). */
+const char* ace_error_string(int code);
+
+/*
+ * Bytes of device workspace ace_forward needs for this problem.  The
+ * workspace holds per-block partial sums and a few ticket counters.  Its first
+ * `ace_workspace_reset_bytes()` bytes must be zero before the first call; every
+ * call leaves them zero again, so a workspace is reused without clearing.
+ * Calls that use the same workspace must be ordered (same stream).
+ */
+size_t ace_workspace_bytes(int64_t batch, int64_t channels, int64_t voxels,
+                           int num_bins, int binning, int x_dtype,
+                           int include_background);
+size_t ace_workspace_reset_bytes(int64_t batch, int64_t channels,
+                                 int64_t voxels, int num_bins, int binning,
+                                 int x_dtype, int include_background);
+
+/*
+ * Forward: per-bin statistics (W, P, G) of every (b, c') slice, then the
+ * epilogue (reference kernels/epilogue.py:23-82 semantics):
+ *   d[b,c',k]    = P/W - G/W for non-empty bins, else 0            [B, C', K]
+ *   coef[b,c',k] = sign(d) / (K_ne * W) for non-empty bins, else 0 [B, C', K]
+ *   per_class    = f * present * w_c   (f = mean |d| over non-empty bins,
+ *                  NaN when every bin is empty)                    [B, C']
+ *   jac          = d(sum of loss outputs) / d f                    [B, C']
+ *   loss[0]      = mean / sum of per_class (unused for reduction NONE)
+ * `bin_table` is the reference's float32 torch.linspace table: hard ->
+ * linspace(0, 1+eps32, K+1)[1:] (K values); soft -> linspace(0, 1+eps32,
+ * 2K+1)[1:] (2K values).  `centre_table` (soft only, else NULL) is
+ * [-1e4, c0, c0, c1, c1, ..., c_{K-1}, c_{K-1}, 1e4] (2K+2 values).
+ * `class_weight` is NULL (unweighted) or C' float32 weights.  `stats`, when not
+ * NULL, receives float64 [3, B, C', K]: W, P, G.
+ */
+int ace_forward(const void* x, int x_dtype, const void* target,
+                int target_kind, int64_t batch, int64_t channels,
+                int64_t voxels, int num_bins, int binning, int activation,
+                int include_background, int ignore_empty_classes,
+                int reduction, int right, float empty_weight,
+                const float* class_weight, const float* bin_table,
+                const float* centre_table, void* workspace,
+                size_t workspace_bytes, float* coef, float* diff, float* jac,
+                float* per_class, float* loss, double* stats, void* stream);
+
+/*
+ * Backward: dx[b,c,n] = d loss / d x for upstream gradient `grad_output`
+ * (one float32 scalar when grad_output_per_class == 0, else [B, C'] values,
+ * reduction NONE).  g = jac * grad_output is formed in-kernel.  `coef`, `diff`
+ * and `jac` are the forward's outputs; `diff` may be NULL for hard binning.
+ * `target` may be NULL for hard binning (the hard gradient does not use it).
+ * dx has the element type of x.
+ */
+int ace_backward(const void* x, int x_dtype, const void* target,
+                 int target_kind, int64_t batch, int64_t channels,
+                 int64_t voxels, int num_bins, int binning, int activation,
+                 int include_background, int right, const float* bin_table,
+                 const float* centre_table, const float* coef,
+                 const float* diff, const float* jac,
+                 const float* grad_output, int grad_output_per_class,
+                 void* dx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ACE_HIP_H */

@@ -1,0 +1,71 @@
+"""The C-ABI library loads and exports every symbol its header declares (CPU).
+
+No kernel is launched here: only host functions (workspace sizing, error
+strings, argument validation that returns before any HIP call).
+"""
+
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+
+from ace_kernels import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "ace_hip.h"
+
+
+def _declared() -> list:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ace_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_exports() -> None:
+    assert _declared() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    lib = _lib.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.ace_abi_version() == _lib.ABI_VERSION
+
+
+def test_error_strings() -> None:
+    lib = _lib.lib()
+    assert lib.ace_error_string(0) == b"success"
+    assert b"invalid" in lib.ace_error_string(1)
+    assert b"workspace" in lib.ace_error_string(3)
+
+
+def test_workspace_sizes() -> None:
+    lib = _lib.lib()
+    small = lib.ace_workspace_bytes(1, 4, 512, 20, _lib.HARD, _lib.F32, 1)
+    big = lib.ace_workspace_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F32, 1)
+    assert 0 < small < big
+    assert big < 64 << 20  # per-block partials only, not voxel-sized
+    reset = lib.ace_workspace_reset_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F32, 1)
+    assert 0 < reset < big and reset % 256 == 0
+    assert lib.ace_workspace_bytes(0, 4, 512, 20, 0, 0, 1) == 0
+
+
+def test_invalid_arguments_rejected_before_launch() -> None:
+    lib = _lib.lib()
+    args = [None, _lib.F32, None, _lib.TARGET_LABELS_I64, 2, 4, 64, 20, _lib.HARD, _lib.ACT_SOFTMAX,
+            1, 1, _lib.RED_MEAN, 0, 0.01, None, None, None, None, 0, None, None, None, None, None, None, None]
+    assert lib.ace_forward(*args) == 1  # null x
+    bwd = [None, _lib.F32, None, 0, 2, 4, 64, 20, _lib.HARD, 1, 1, 0, None, None, None, None, None, None, 0, None, None]
+    assert lib.ace_backward(*bwd) == 1
+
+
+def test_missing_library_fails_loudly(monkeypatch: pytest.MonkeyPatch, tmp_path: Path) -> None:
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    _lib.lib.cache_clear()
+    try:
+        with pytest.raises(_lib.AceLibraryError, match="not built"):
+            _lib.lib()
+    finally:
+        monkeypatch.undo()
+        _lib.lib.cache_clear()

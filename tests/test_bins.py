@@ -1,0 +1,104 @@
+"""The kernels' O(1) bin index (``ace::bucket``) equals torch.bucketize.
+
+The reference's v6 kernels use ``floor(p * n)`` plus two correction rounds
+(``src/ace_kernels/kernels/bins.py:27-48``) and test them at every float32
+within 8 ulp of every edge (``tests/test_triton.py:352-393``).  The HIP kernels
+use one round (both neighbours read at once).  This test compiles the very
+header the kernels include (``csrc/ace_bins.hpp``) with g++ and checks it
+against a binary search over the same float32 ``torch.linspace`` tables:
+
+- every float32 within 4096 ulp of every edge, for K in 1..128 and larger K,
+  hard (K edges) and soft (2K half boundaries), right = False / True;
+- every float32 in [0, 1 + eps32] (exhaustive) for the benchmark tables
+  K = 20 and K = 50;
+- out-of-domain values (NaN, +-inf, > 1) stay inside [0, n - 1].
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE.parent / "ace-kernels_amd" / "csrc"
+EPS32 = torch.finfo(torch.float32).eps
+
+
+@pytest.fixture(scope="module")
+def harness(tmp_path_factory) -> ctypes.CDLL:
+    out = tmp_path_factory.mktemp("bins") / "libbins.so"
+    cmd = ["g++", "-O2", "-fopenmp", "-shared", "-fPIC", "-std=c++17", f"-I{CSRC}",
+           str(HERE / "bins_harness.cpp"), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True)
+    lib = ctypes.CDLL(str(out))
+    fp = ctypes.POINTER(ctypes.c_float)
+    lib.check_values.restype = ctypes.c_longlong
+    lib.check_values.argtypes = [fp, ctypes.c_int, ctypes.c_int, fp, ctypes.c_longlong]
+    lib.check_near_edges.restype = ctypes.c_longlong
+    lib.check_near_edges.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.check_range.restype = ctypes.c_longlong
+    lib.check_range.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+    lib.check_clamped.restype = ctypes.c_int
+    lib.check_clamped.argtypes = [fp, ctypes.c_int]
+    return lib
+
+
+def _table(n_bins: int, soft: bool) -> np.ndarray:
+    steps = (2 * n_bins if soft else n_bins) + 1
+    return torch.linspace(0.0, 1.0 + EPS32, steps)[1:].numpy().astype(np.float32).copy()
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+KS = list(range(1, 129)) + [200, 256, 333, 500, 1000, 4096]
+
+
+@pytest.mark.parametrize("soft", [False, True])
+@pytest.mark.parametrize("right", [False, True])
+def test_near_every_edge(harness, soft: bool, right: bool) -> None:
+    bad = {}
+    for k in KS:
+        t = _table(k, soft)
+        n = harness.check_near_edges(_fp(t), t.size, int(right), 4096)
+        if n:
+            bad[k] = n
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("k", [20, 50])
+@pytest.mark.parametrize("soft", [False, True])
+def test_exhaustive_unit_interval(harness, k: int, soft: bool) -> None:
+    t = _table(k, soft)
+    for right in (0, 1):
+        assert harness.check_range(_fp(t), t.size, right, 0.0, float(1.0 + EPS32)) == 0
+
+
+def test_random_and_out_of_domain(harness) -> None:
+    gen = np.random.default_rng(0)
+    p = gen.random(1_000_000, dtype=np.float32)
+    for k in (1, 3, 20, 50, 100):
+        for soft in (False, True):
+            t = _table(k, soft)
+            for right in (0, 1):
+                assert harness.check_values(_fp(t), t.size, right, _fp(p), p.size) == 0
+            assert harness.check_clamped(_fp(t), t.size) == 1
+
+
+def test_edges_detect_an_uncorrected_index(harness) -> None:
+    """Planted mistake: floor(p * n) alone (no correction) must fail near edges,
+    so the near-edge sweep above is sensitive to a missing correction."""
+    harness.check_near_edges_uncorrected.restype = ctypes.c_longlong
+    harness.check_near_edges_uncorrected.argtypes = [
+        ctypes.POINTER(ctypes.c_float), ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    total = 0
+    for k in (3, 7, 20, 50):
+        t = _table(k, False)
+        total += harness.check_near_edges_uncorrected(_fp(t), t.size, 0, 8)
+    assert total > 0

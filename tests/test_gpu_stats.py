@@ -1,0 +1,112 @@
+"""Per-bin statistics of the HIP forward vs the oracle (exact counts, accurate sums).
+
+With activation "none" the kernel bins exactly the probabilities the oracle
+bins, so counts W and target sums G (hard) must be bit-exact and P within
+float32 summation error of the float64 truth (upstream tests/test_triton.py:
+23-105, 175-208).  With softmax, bins may differ only where the in-kernel
+probability lies within an ulp of an edge; those voxels are counted.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from ace_kernels import ACEConfig
+from gpu_helpers import cpu_probs, hip_stats, onehot_np, say
+from oracle import f64
+
+pytestmark = pytest.mark.gpu
+
+SPATIAL = {"n1": (1,), "n7": (7,), "n100003": (100003,), "cube": (24, 24, 24)}
+
+
+def _inputs(kind: str, b: int, c: int, spatial, seed: int, num_bins: int):
+    gen = torch.Generator().manual_seed(seed)
+    shape = (b, c, *spatial)
+    if kind == "logits":
+        x = torch.randn(shape, generator=gen) * 2.0
+    elif kind == "probs":
+        x = torch.rand(shape, generator=gen)
+    elif kind == "bin_edges":
+        edges = torch.arange(num_bins + 1, dtype=torch.float32) / num_bins
+        x = edges[torch.randint(0, num_bins + 1, shape, generator=gen)]
+    else:  # extreme
+        x = torch.randint(0, 2, shape, generator=gen).float()
+    labels = torch.randint(0, c, (b, 1, *spatial), generator=gen)
+    return x, labels
+
+
+def _truth(x, y, config):
+    c = x.shape[1]
+    p = cpu_probs(x, config).reshape(x.shape[0], c, -1).double().numpy()
+    yy = onehot_np(y, c, config)
+    if not config.include_background and c > 1:
+        p, yy = p[:, 1:], yy[:, 1:]
+    return f64.stats64(p, yy, config)
+
+
+@pytest.mark.parametrize("spatial", sorted(SPATIAL))
+@pytest.mark.parametrize("channels", [1, 4, 16])
+@pytest.mark.parametrize("num_bins", [1, 20, 50])
+@pytest.mark.parametrize("right", [False, True])
+@pytest.mark.parametrize("kind", ["probs", "bin_edges", "extreme"])
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_stats_exact_on_given_probabilities(binning, kind, right, num_bins, channels, spatial) -> None:
+    config = ACEConfig(binning=binning, num_bins=num_bins, right=right, activation="none")
+    x, labels = _inputs(kind, 2, channels, SPATIAL[spatial], 3, num_bins)
+    y = torch.zeros(x.shape).scatter_(1, labels, 1.0)  # one-hot float targets
+    say(f"stats {binning} {kind} right={right} K={num_bins} C={channels} {spatial}")
+    *_, st = hip_stats(x.cuda(), y.cuda(), config)
+    st = st.cpu().numpy()
+    w, sp, sg = _truth(x, y, config)
+    if binning == "hard":
+        np.testing.assert_array_equal(st[0], w)
+        np.testing.assert_array_equal(st[2], sg)
+        np.testing.assert_allclose(st[1], sp, rtol=0, atol=2.0 ** -31 * max(1, x[0, 0].numel()))
+    else:
+        # fixed-point sums of float32 terms: within 2^-31 per term of the float64
+        # interpolation weights plus float32 rounding of each weight (~6e-8 each)
+        n = x[0, 0].numel()
+        tol = 1e-6 * np.maximum(1.0, np.abs(w)) + 2.0 ** -31 * n
+        np.testing.assert_allclose(st[0], w, rtol=0, atol=tol.max())
+        np.testing.assert_allclose(st[1], sp, rtol=0, atol=tol.max())
+        np.testing.assert_allclose(st[2], sg, rtol=0, atol=tol.max())
+
+
+@pytest.mark.parametrize("include_background", [True, False])
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_stats_with_labels_and_softmax(binning, include_background) -> None:
+    """Index targets (fused one-hot) and in-kernel softmax; background dropped."""
+    config = ACEConfig(binning=binning, to_onehot_y=True, include_background=include_background)
+    x, labels = _inputs("logits", 2, 5, (40, 40, 9), 5, 20)
+    say(f"stats labels {binning} bg={include_background}")
+    *_, st = hip_stats(x.cuda(), labels.cuda(), config)
+    st = st.cpu().numpy()
+    w, sp, sg = _truth(x, labels, config)
+    n = x[0, 0].numel()
+    if binning == "hard":
+        # bins can move only for probabilities within an ulp of an edge
+        moved = np.abs(st[0] - w).sum()
+        assert moved <= 4, moved
+        assert st[0].sum() == w.sum()
+        assert st[2].sum() == sg.sum()  # every labelled voxel counted once
+        np.testing.assert_allclose(st[1], sp, rtol=0, atol=1e-5 * max(1.0, np.abs(sp).max()))
+    else:
+        np.testing.assert_allclose(st[0].sum(-1), n, rtol=1e-6)  # weights sum to 1 per voxel
+        np.testing.assert_allclose(st[2].sum(-1), sg.sum(-1), rtol=1e-6, atol=1e-4)
+        np.testing.assert_allclose(st[0], w, rtol=0, atol=1e-4)
+        np.testing.assert_allclose(st[1], sp, rtol=0, atol=1e-4)
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_forward_is_bitwise_deterministic(binning) -> None:
+    config = ACEConfig(binning=binning, to_onehot_y=True)
+    x, labels = _inputs("logits", 2, 4, (64, 64, 64), 9, 20)
+    x, labels = x.cuda(), labels.cuda()
+    say(f"determinism {binning}")
+    outs = [hip_stats(x, labels, config) for _ in range(3)]
+    for o in outs[1:]:
+        for a, b in zip(o, outs[0]):
+            assert torch.equal(a, b)
