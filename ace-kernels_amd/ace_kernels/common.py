@@ -70,20 +70,30 @@ def class_weight_tensor(weights: Tuple[float, ...], device: torch.device) -> tor
 
 
 _WS_LOCK = threading.Lock()
-_WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+_WORKSPACES: Dict[Tuple[int, int], list] = {}
 
 
-def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    """A zero-initialised uint8 device buffer of at least ``nbytes`` for ``stream``.
+def workspace(device: torch.device, stream: int, nbytes: int, reset_bytes: int) -> torch.Tensor:
+    """A uint8 device buffer of at least ``nbytes`` for ``stream`` whose first
+    ``reset_bytes`` bytes are zero when the next forward on ``stream`` runs.
 
     One buffer per (device, stream): forwards on one stream are ordered, so
-    they can share it; forwards on different streams get different buffers.
+    they share it; forwards on different streams get different buffers.  Every
+    forward leaves its own reset region (ticket counters and final sums) zero
+    and writes its per-block partials right after it, so the leading
+    ``clean`` bytes of the buffer are known to be zero, where ``clean`` is the
+    reset size of the last forward; a forward that needs more is preceded by
+    one fill of its reset region (only when the problem's layout grows).
     """
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     with _WS_LOCK:
-        buf = _WORKSPACES.get(key)
-        if buf is None or buf.numel() < nbytes:
-            size = max(nbytes, 1 << 20)
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
-            _WORKSPACES[key] = buf
+        entry = _WORKSPACES.get(key)
+        if entry is None or entry[0].numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            entry = [buf, buf.numel()]
+            _WORKSPACES[key] = entry
+        buf, clean = entry
+        if reset_bytes > clean:
+            buf[:reset_bytes].zero_()
+        entry[1] = reset_bytes
         return buf

@@ -37,6 +37,13 @@ int env_steps(const char* name) {
   return s > 0 && s <= 1024 ? s : 0;
 }
 
+// Cross-block reduction: "tree" (group tickets, default) or "direct"
+// (every block adds its partial to the final sums with integer atomics).
+int env_reduce_mode() {
+  const char* v = getenv("ACE_FWD_REDUCE");
+  return (v && v[0] == 'd') ? kReduceDirect : kReduceTree;
+}
+
 size_t elem_size(int dtype) { return dtype == ACE_F32 ? 4 : 2; }
 
 bool aligned_to(const void* p, size_t a) {
@@ -159,8 +166,10 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   p.clsw = class_weight;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   p.ctr = reinterpret_cast<int*>(ws);
+  p.fin = reinterpret_cast<unsigned long long*>(ws + g.off_fin);
   p.part = reinterpret_cast<long long*>(ws + g.off_part);
-  p.gpart = reinterpret_cast<long long*>(ws + g.off_gpart);
+  p.mode = env_reduce_mode();
+  p.epi_batch = g.epi_batch;
   p.coef = coef;
   p.d = diff;
   p.jac = jac;

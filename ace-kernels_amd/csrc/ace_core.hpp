@@ -38,6 +38,7 @@ namespace ace {
 enum { kActNone = 0, kActSoftmax = 1, kActSigmoid = 2 };
 enum { kRedMean = 0, kRedSum = 1, kRedNone = 2 };
 enum { kTgtLabels = 0, kTgtOnehot = 1 };
+enum { kReduceTree = 0, kReduceDirect = 1 };
 
 struct FwdParams {
   const void* x;
@@ -48,12 +49,14 @@ struct FwdParams {
   int64_t gs;
   int64_t gpb;
   int B, C, off, K, act, tk, right, copies, vec_ok, ignore_empty, red;
+  int mode;            // kReduceTree or kReduceDirect
+  int epi_batch;       // batch indices per epilogue pass
   float empty_w;
   const float* btab;   // bucket table (K or 2K upper boundaries)
   const float* rtab;   // soft centre table (2K + 2)
   const float* clsw;   // C' class weights or null
-  long long* part;     // [nblk][3][CK]
-  long long* gpart;    // [B * gpb][3][CK]
+  long long* part;     // [nblk][3][CK] block partials (tree mode)
+  unsigned long long* fin;  // [B][3][CK] zeroed final sums (reset by the epilogue)
   int* ctr;            // [B * gpb + 1] zeroed ticket counters
   float* coef;
   float* d;
@@ -224,6 +227,32 @@ __device__ __forceinline__ void lds_add(unsigned int* p, unsigned int v) {
   __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// Cross-block communication without cache-wide fences.  An agent-scope
+// fence on gfx950 writes back and invalidates the whole L2 (buffer_wbl2 sc1 /
+// buffer_inv sc1), which thousands of blocks cannot afford.  Instead every
+// value another block reads is written and read with device-coherent (sc1)
+// accesses -- relaxed agent-scope atomic stores/loads -- or integer atomics; a
+// block waits for its own writes to complete (s_waitcnt vmcnt(0)) before it
+// increments a ticket, and the block that draws the last ticket reads the data
+// with sc1 loads.  No dirty L2 line holds shared data, so no write-back is
+// needed, and no stale line can be read.
+__device__ __forceinline__ void store_dev(long long* p, long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long load_dev(const unsigned long long* p) {
+  return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this thread's global stores and atomics have completed.
+__device__ __forceinline__ void wait_own_writes() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ int ticket(int* ctr) {
+  return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Copies the bucket table (padded with -inf / +inf) and the centre table into
 // LDS; returns pointers to both.
 __device__ __forceinline__ void load_tables(float* lds, const float* btab, const float* rtab,
@@ -372,8 +401,11 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
   }
   __syncthreads();
 
-  // ---- block partial: sum the copies, 3 x CK fixed-point values
-  long long* part = P.part + blk * 3 * (int64_t)CK;
+  // ---- block partial: sum the copies -> W3 = 3 x CK fixed-point values
+  const int W3 = 3 * CK;
+  const bool direct = P.mode == kReduceDirect;
+  unsigned long long* fin_b = P.fin + (int64_t)b * W3;
+  long long* part = P.part + blk * (int64_t)W3;
   for (int t = tid; t < CK; t += kThreads) {
     long long s0 = 0, s1 = 0, s2 = 0;
     for (int r = 0; r < R; ++r) {
@@ -390,65 +422,94 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
         s2 += histG[slot];
       }
     }
-    part[t] = s0;
-    part[CK + t] = s1;
-    part[2 * CK + t] = s2;
-  }
-
-  // ---- ticket: the last block of the group reduces the group
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  const int64_t g = tile / P.gs;
-  const int64_t gidx = (int64_t)b * P.gpb + g;
-  const int64_t gsize = min(P.gs, P.tiles - g * P.gs);
-  if (tid == 0) {
-    const int prev = atomicAdd(&P.ctr[gidx], 1);
-    s_last = (prev == (int)gsize - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  {
-    const long long* src = P.part + ((int64_t)b * P.tiles + g * P.gs) * 3 * (int64_t)CK;
-    long long* dst = P.gpart + gidx * 3 * (int64_t)CK;
-    for (int t = tid; t < 3 * CK; t += kThreads) {
-      long long s = 0;
-      for (int64_t i = 0; i < gsize; ++i) s += src[i * 3 * (int64_t)CK + t];
-      dst[t] = s;
+    if (direct) {
+      // integer atomics into the final sums: order-independent, deterministic
+      if (s0) atomicAdd(&fin_b[t], (unsigned long long)s0);
+      if (s1) atomicAdd(&fin_b[CK + t], (unsigned long long)s1);
+      if (s2) atomicAdd(&fin_b[2 * CK + t], (unsigned long long)s2);
+    } else {
+      store_dev(&part[t], s0);
+      store_dev(&part[CK + t], s1);
+      store_dev(&part[2 * CK + t], s2);
     }
   }
-  if (tid == 0) atomicExch(&P.ctr[gidx], 0);
-  __threadfence();
+
+  __shared__ int s_last;
+  wait_own_writes();
   __syncthreads();
-  const int64_t ngroups = (int64_t)P.B * P.gpb;
+  const int64_t ngroups = (int64_t)P.B * P.gpb;  // index of the top counter
+  int64_t arrivals = P.B * P.tiles;              // direct: every block reports
+  if (!direct) {
+    // ---- group ticket: the last block of the group sums the group's rows
+    const int64_t g = tile / P.gs;
+    const int64_t gidx = (int64_t)b * P.gpb + g;
+    const int64_t gsize = min(P.gs, P.tiles - g * P.gs);
+    if (tid == 0) {
+      const int prev = ticket(&P.ctr[gidx]);
+      s_last = (prev == (int)gsize - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    unsigned long long* acc = reinterpret_cast<unsigned long long*>(hist);
+    for (int t = tid; t < W3; t += kThreads) acc[t] = 0ull;
+    __syncthreads();
+    // the group's partials are gsize contiguous rows of W3 values: read them
+    // with every thread, four independent loads in flight per thread
+    const unsigned long long* src = reinterpret_cast<const unsigned long long*>(
+        P.part + ((int64_t)b * P.tiles + g * P.gs) * W3);
+    const int total = (int)gsize * W3;
+    for (int i0 = tid; i0 < total; i0 += 4 * kThreads) {
+      unsigned long long v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * kThreads;
+        v[u] = i < total ? load_dev(src + i) : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (v[u]) lds_add(&acc[(i0 + u * kThreads) % W3], v[u]);
+    }
+    __syncthreads();
+    for (int t = tid; t < W3; t += kThreads)
+      if (acc[t]) atomicAdd(&fin_b[t], acc[t]);
+    if (tid == 0) __hip_atomic_store(&P.ctr[gidx], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_own_writes();
+    __syncthreads();
+    arrivals = ngroups;
+  }
+  // ---- top ticket: the last arrival runs the epilogue
   if (tid == 0) {
-    const int prev = atomicAdd(&P.ctr[ngroups], 1);
-    s_last = (prev == (int)ngroups - 1);
+    const int prev = ticket(&P.ctr[ngroups]);
+    s_last = (prev == (int)arrivals - 1);
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
 
-  // ---- epilogue (one block): per batch index, statistics -> outputs
+  // ---- epilogue (one block), `bc` batch indices at a time:
+  // sums -> d, W, G per bin (LDS); per (b, c') row: K_ne, f, coef, jac
+  const int bc = P.epi_batch;
   float* sd = reinterpret_cast<float*>(hist);
-  float* sw = sd + CK;
-  float* sg = sw + CK;
-  float* sf = sg + CK;
-  unsigned char* se = reinterpret_cast<unsigned char*>(sf + CK);
+  float* sw = sd + (size_t)bc * CK;
+  float* sg = sw + (size_t)bc * CK;
+  float* sf = sg + (size_t)bc * CK;
+  unsigned char* se = reinterpret_cast<unsigned char*>(sf + (size_t)bc * CK);
   const int64_t BCK = (int64_t)P.B * CK;
   const double dscale = 1.0 / 1073741824.0;
   const int rows = P.B * CL;
   float total = 0.0f;  // thread 0: sequential sum of the per-class errors
-  for (int bb = 0; bb < P.B; ++bb) {
-    for (int t = tid; t < CK; t += kThreads) {
-      long long s0 = 0, s1 = 0, s2 = 0;
-      const long long* src = P.gpart + (int64_t)bb * P.gpb * 3 * (int64_t)CK;
-      for (int64_t gi = 0; gi < P.gpb; ++gi) {
-        s0 += src[gi * 3 * (int64_t)CK + t];
-        s1 += src[gi * 3 * (int64_t)CK + CK + t];
-        s2 += src[gi * 3 * (int64_t)CK + 2 * CK + t];
-      }
+  for (int b0 = 0; b0 < P.B; b0 += bc) {
+    const int nb = min(bc, P.B - b0);
+    for (int i = tid; i < nb * CK; i += kThreads) {
+      const int bb = b0 + i / CK;
+      const int t = i - (i / CK) * CK;
+      unsigned long long* fb = P.fin + (int64_t)bb * W3;
+      const long long s0 = (long long)load_dev(&fb[t]);
+      const long long s1 = (long long)load_dev(&fb[CK + t]);
+      const long long s2 = (long long)load_dev(&fb[2 * CK + t]);
+      // leave the accumulator zero for the next call
+      __hip_atomic_store(&fb[t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&fb[CK + t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&fb[2 * CK + t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const double Wd = (double)s0 * dscale;
       const double Pd = (double)s1 * dscale;
       const double Gd = (double)s2 * dscale;
@@ -462,32 +523,33 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
       const float Gf = (float)Gd;
       const bool empty = SOFT ? !(Wf >= P.empty_w) : (Wf == 0.0f);
       const float dd = empty ? 0.0f : (Pf / Wf - Gf / Wf);
-      sd[t] = dd;
-      sw[t] = Wf;
-      sg[t] = Gf;
-      se[t] = empty ? 1 : 0;
+      sd[i] = dd;
+      sw[i] = Wf;
+      sg[i] = Gf;
+      se[i] = empty ? 1 : 0;
       P.d[(int64_t)bb * CK + t] = dd;
     }
     __syncthreads();
-    for (int cl = tid; cl < CL; cl += kThreads) {
+    for (int r = tid; r < nb * CL; r += kThreads) {
+      const int bb = b0 + r / CL;
+      const int cl = r - (r / CL) * CL;
+      const int base = (r / CL) * CK + cl * K;
       int kne = 0;
       float err = 0.0f, gsum = 0.0f;
       for (int k = 0; k < K; ++k) {
-        const int t = cl * K + k;
-        if (!se[t]) {
+        if (!se[base + k]) {
           ++kne;
-          err += fabsf(sd[t]);
+          err += fabsf(sd[base + k]);
         }
-        gsum += sg[t];
+        gsum += sg[base + k];
       }
       const float fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
       const float present = gsum > 0.0f ? 1.0f : 0.0f;
       const float kf = (float)(kne > 0 ? kne : 1);
       for (int k = 0; k < K; ++k) {
-        const int t = cl * K + k;
-        const float dd = sd[t];
+        const float dd = sd[base + k];
         const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
-        P.coef[(int64_t)bb * CK + t] = se[t] ? 0.0f : sgn / (kf * sw[t]);
+        P.coef[(int64_t)bb * CK + cl * K + k] = se[base + k] ? 0.0f : sgn / (kf * sw[base + k]);
       }
       const float w = P.clsw ? P.clsw[cl] : 1.0f;
       float fw = P.ignore_empty ? fcls * present : fcls;
@@ -496,17 +558,17 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
       if (P.red == kRedMean) jac = jac / (float)rows;
       P.f[bb * CL + cl] = fw;
       P.jac[bb * CL + cl] = jac;
-      sf[cl] = fw;
+      sf[r] = fw;
     }
     __syncthreads();
     if (tid == 0)
-      for (int cl = 0; cl < CL; ++cl) total += sf[cl];
+      for (int r = 0; r < nb * CL; ++r) total += sf[r];
     __syncthreads();
   }
   if (tid == 0) {
     if (P.red == kRedMean) total = total / (float)rows;
     if (P.red != kRedNone) P.loss[0] = total;
-    atomicExch(&P.ctr[ngroups], 0);
+    __hip_atomic_store(&P.ctr[ngroups], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

@@ -58,8 +58,9 @@ struct Geometry {
   size_t tab_floats;   // padded bucket table (n + 2) + centre table (2K + 2)
   size_t lds_fwd;      // dynamic LDS of the forward kernel
   size_t lds_bwd;      // dynamic LDS of the backward kernel
-  size_t ws_counters;  // bytes of ticket counters (must start zeroed)
-  size_t off_part, off_gpart, ws_bytes;
+  int epi_batch;       // batch indices per epilogue pass
+  size_t ws_counters;  // bytes that must start zeroed (counters + final sums)
+  size_t off_fin, off_part, ws_bytes;
 };
 
 // Blocks per batch index: aim for ~8 blocks per CU on a 256-CU part while
@@ -101,20 +102,29 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   g.copies = copies;
   const int n = soft ? 2 * K : K;
   g.tab_floats = align_up((size_t)(n + 2) + (soft ? (size_t)(2 * K + 2) : 0), 4);
-  // the last block reuses the histogram region for the epilogue:
-  // d, W, G, per-class f (float) and an empty flag per bin of one batch index
-  const size_t epi = align_up((size_t)g.ck * 17, 16);
+  // the group-last block sums rows into 3 x CK u64 (LDS), and the last block
+  // reuses the histogram region for the epilogue: d, W, G, per-class f
+  // (float) and an empty flag per bin, for `epi_batch` batch indices at a time
   const size_t hist = align_up(per_copy * copies, 16);
-  g.lds_fwd = g.tab_floats * 4 + (hist > epi ? hist : epi);
+  const size_t acc = align_up((size_t)g.ck * 24, 16);
+  const size_t region = hist > acc ? hist : acc;
+  int64_t eb = (int64_t)(region / ((size_t)g.ck * 17));
+  if (eb < 1) eb = 1;
+  if (eb > B) eb = B;
+  g.epi_batch = (int)eb;
+  g.lds_fwd = g.tab_floats * 4 + region;
   // backward: tables + coef (+ d) + g
   g.lds_bwd = g.tab_floats * 4 + align_up((size_t)g.ck * (soft ? 2 : 1) + g.CL, 4) * 4;
+  // workspace: [ticket counters | final sums] must start zero and are left
+  // zero by every call; then the per-block partials
   const int64_t counters = B * g.gpb + 1;
-  g.ws_counters = align_up((size_t)counters * sizeof(int), 256);
+  const size_t ctr_bytes = align_up((size_t)counters * sizeof(int), 256);
+  const size_t fin_bytes = align_up((size_t)B * 3 * g.ck * sizeof(unsigned long long), 256);
+  g.off_fin = ctr_bytes;
+  g.ws_counters = ctr_bytes + fin_bytes;
   const size_t part_bytes = (size_t)g.nblk * 3 * g.ck * sizeof(long long);
-  const size_t gpart_bytes = (size_t)(B * g.gpb) * 3 * g.ck * sizeof(long long);
   g.off_part = g.ws_counters;
-  g.off_gpart = align_up(g.off_part + part_bytes, 256);
-  g.ws_bytes = align_up(g.off_gpart + gpart_bytes, 256);
+  g.ws_bytes = align_up(g.off_part + part_bytes, 256);
   return g;
 }
 

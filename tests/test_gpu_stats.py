@@ -110,3 +110,25 @@ def test_forward_is_bitwise_deterministic(binning) -> None:
     for o in outs[1:]:
         for a, b in zip(o, outs[0]):
             assert torch.equal(a, b)
+
+
+def test_workspace_reuse_across_problem_sizes() -> None:
+    """One stream's cached workspace serves problems whose layouts differ: a
+    larger reset region must not inherit a smaller problem's partials."""
+    from ace_kernels import common
+
+    shapes = [(1, 4, (8, 8, 8)), (2, 4, (64, 64, 32)), (1, 3, (20, 20)), (4, 16, (32, 32, 8)), (2, 4, (64, 64, 32))]
+    runs = []
+    for binning in ("hard", "soft"):
+        for b, c, sp in shapes:
+            config = ACEConfig(binning=binning, to_onehot_y=True, num_bins=20 if c != 3 else 7)
+            x, labels = _inputs("logits", b, c, sp, 11, 20)
+            runs.append((config, x.cuda(), labels.cuda()))
+    say("workspace reuse: interleaved shapes")
+    first = [hip_stats(x, y, cfg) for cfg, x, y in runs]
+    common._WORKSPACES.clear()  # fresh buffers, each problem alone
+    for (cfg, x, y), ref in zip(runs, first):
+        common._WORKSPACES.clear()
+        again = hip_stats(x, y, cfg)
+        for a, r in zip(again, ref):
+            assert torch.equal(a, r)
