@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enums of include/ace_hip.h
 F32, BF16, F16 = 0, 1, 2
@@ -62,7 +62,7 @@ def lib() -> ctypes.CDLL:
     for name in ("ace_workspace_bytes", "ace_workspace_reset_bytes"):
         fn = getattr(handle, name)
         fn.restype = _sz
-        fn.argtypes = [_i64, _i64, _i64, _i, _i, _i, _i]
+        fn.argtypes = [_i64, _i64, _i64, _i, _i, _i, _i, _i]
     handle.ace_forward.restype = _i
     handle.ace_forward.argtypes = [
         _p, _i, _p, _i,            # x, dtype, target, kind

@@ -114,7 +114,7 @@ def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False):
     dev = pl.x.device
     stream = torch.cuda.current_stream(dev).cuda_stream
     binning = _lib.SOFT if pl.soft else _lib.HARD
-    dims = (pl.B, pl.C, pl.N, pl.K, binning, pl.dtype_code, int(pl.include_bg))
+    dims = (pl.B, pl.C, pl.N, pl.K, binning, pl.dtype_code, int(pl.include_bg), pl.target_kind)
     ws = workspace(dev, stream, lib.ace_workspace_bytes(*dims), lib.ace_workspace_reset_bytes(*dims))
     f32 = torch.float32
     coef = torch.empty((pl.B, pl.CL, pl.K), dtype=f32, device=dev)

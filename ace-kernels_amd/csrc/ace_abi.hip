@@ -14,16 +14,50 @@
 #include "ace_hip.h"
 
 namespace ace {
-#define ACE_DECLARE_LAUNCHERS(T, SOFT)                                                          \
-  template <> hipError_t launch_variant_fwd<T, SOFT>(const Geometry&, const FwdParams&, hipStream_t); \
-  template <> hipError_t launch_variant_bwd<T, SOFT>(const Geometry&, const BwdParams&, hipStream_t);
-ACE_DECLARE_LAUNCHERS(float, false)
-ACE_DECLARE_LAUNCHERS(float, true)
-ACE_DECLARE_LAUNCHERS(__hip_bfloat16, false)
-ACE_DECLARE_LAUNCHERS(__hip_bfloat16, true)
-ACE_DECLARE_LAUNCHERS(__half, false)
-ACE_DECLARE_LAUNCHERS(__half, true)
+#define ACE_DECLARE_LAUNCHERS(T, SOFT, RIGHT)                                                \
+  template <> hipError_t launch_variant_fwd<T, SOFT, RIGHT>(const Geometry&, const FwdParams&, \
+                                                            hipStream_t);                    \
+  template <> hipError_t launch_variant_bwd<T, SOFT, RIGHT>(const Geometry&, const BwdParams&, \
+                                                            hipStream_t);
+#define ACE_DECLARE_BOTH(T, SOFT) ACE_DECLARE_LAUNCHERS(T, SOFT, false) ACE_DECLARE_LAUNCHERS(T, SOFT, true)
+ACE_DECLARE_BOTH(float, false)
+ACE_DECLARE_BOTH(float, true)
+ACE_DECLARE_BOTH(__hip_bfloat16, false)
+ACE_DECLARE_BOTH(__hip_bfloat16, true)
+ACE_DECLARE_BOTH(__half, false)
+ACE_DECLARE_BOTH(__half, true)
+#undef ACE_DECLARE_BOTH
 #undef ACE_DECLARE_LAUNCHERS
+
+// Dispatch on (element type, binning, right) to the instantiated launchers.
+template <typename T>
+hipError_t pick_fwd(bool soft, bool right, const Geometry& g, const FwdParams& p, hipStream_t s) {
+  if (soft)
+    return right ? launch_variant_fwd<T, true, true>(g, p, s) : launch_variant_fwd<T, true, false>(g, p, s);
+  return right ? launch_variant_fwd<T, false, true>(g, p, s) : launch_variant_fwd<T, false, false>(g, p, s);
+}
+template <typename T>
+hipError_t pick_bwd(bool soft, bool right, const Geometry& g, const BwdParams& p, hipStream_t s) {
+  if (soft)
+    return right ? launch_variant_bwd<T, true, true>(g, p, s) : launch_variant_bwd<T, true, false>(g, p, s);
+  return right ? launch_variant_bwd<T, false, true>(g, p, s) : launch_variant_bwd<T, false, false>(g, p, s);
+}
+hipError_t dispatch_fwd(int dtype, bool soft, bool right, const Geometry& g, const FwdParams& p,
+                        hipStream_t s) {
+  switch (dtype) {
+    case ACE_F32: return pick_fwd<float>(soft, right, g, p, s);
+    case ACE_BF16: return pick_fwd<__hip_bfloat16>(soft, right, g, p, s);
+    default: return pick_fwd<__half>(soft, right, g, p, s);
+  }
+}
+hipError_t dispatch_bwd(int dtype, bool soft, bool right, const Geometry& g, const BwdParams& p,
+                        hipStream_t s) {
+  switch (dtype) {
+    case ACE_F32: return pick_bwd<float>(soft, right, g, p, s);
+    case ACE_BF16: return pick_bwd<__hip_bfloat16>(soft, right, g, p, s);
+    default: return pick_bwd<__half>(soft, right, g, p, s);
+  }
+}
 
 namespace {
 
@@ -35,6 +69,14 @@ int env_steps(const char* name) {
   if (!v) return 0;
   const int s = atoi(v);
   return s > 0 && s <= 1024 ? s : 0;
+}
+
+// Tuning knob for experiments: histogram copies per block (power of two <= 64).
+int env_copies() {
+  const char* v = getenv("ACE_FWD_COPIES");
+  if (!v) return 0;
+  const int c = atoi(v);
+  return (c == 1 || c == 2 || c == 4 || c == 8 || c == 16 || c == 32 || c == 64) ? c : 0;
 }
 
 // Cross-block reduction: "tree" (group tickets, default) or "direct"
@@ -81,7 +123,7 @@ using namespace ace;
 
 extern "C" {
 
-int ace_abi_version(void) { return 1; }
+int ace_abi_version(void) { return 2; }
 
 const char* ace_error_string(int code) {
   switch (code) {
@@ -96,21 +138,25 @@ const char* ace_error_string(int code) {
 }
 
 size_t ace_workspace_bytes(int64_t batch, int64_t channels, int64_t voxels, int num_bins,
-                           int binning, int x_dtype, int include_background) {
+                           int binning, int x_dtype, int include_background, int target_kind) {
   (void)x_dtype;
   if (batch < 1 || channels < 1 || voxels < 0 || num_bins < 1) return 0;
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, binning == ACE_SOFT,
-                                   include_background != 0, true, env_steps("ACE_FWD_STEPS"));
+                                   include_background != 0,
+                                   target_kind == ACE_TARGET_LABELS_I64,
+                                   env_steps("ACE_FWD_STEPS"), env_copies());
   return g.ws_bytes;
 }
 
 size_t ace_workspace_reset_bytes(int64_t batch, int64_t channels, int64_t voxels,
                                  int num_bins, int binning, int x_dtype,
-                                 int include_background) {
+                                 int include_background, int target_kind) {
   (void)x_dtype;
   if (batch < 1 || channels < 1 || voxels < 0 || num_bins < 1) return 0;
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, binning == ACE_SOFT,
-                                   include_background != 0, true, env_steps("ACE_FWD_STEPS"));
+                                   include_background != 0,
+                                   target_kind == ACE_TARGET_LABELS_I64,
+                                   env_steps("ACE_FWD_STEPS"), env_copies());
   return g.ws_counters;
 }
 
@@ -131,7 +177,8 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   const bool soft = binning == ACE_SOFT;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
-                                   include_background != 0, labels, env_steps("ACE_FWD_STEPS"));
+                                   include_background != 0, labels, env_steps("ACE_FWD_STEPS"),
+                                   env_copies());
   if (workspace_bytes < g.ws_bytes) return ACE_EWORKSPACE;
   if (g.lds_fwd > kMaxLds) return ACE_EUNSUPPORTED;
   if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
@@ -155,7 +202,6 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   p.K = num_bins;
   p.act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
   p.tk = labels ? kTgtLabels : kTgtOnehot;
-  p.right = right != 0;
   p.copies = g.copies;
   p.vec_ok = vec_ok ? 1 : 0;
   p.ignore_empty = ignore_empty_classes != 0;
@@ -177,21 +223,7 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   p.loss = loss;
   p.stats = stats;
 
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  switch (x_dtype) {
-    case ACE_F32:
-      e = soft ? launch_variant_fwd<float, true>(g, p, s) : launch_variant_fwd<float, false>(g, p, s);
-      break;
-    case ACE_BF16:
-      e = soft ? launch_variant_fwd<__hip_bfloat16, true>(g, p, s)
-               : launch_variant_fwd<__hip_bfloat16, false>(g, p, s);
-      break;
-    default:
-      e = soft ? launch_variant_fwd<__half, true>(g, p, s) : launch_variant_fwd<__half, false>(g, p, s);
-      break;
-  }
-  return to_code(e);
+  return to_code(dispatch_fwd(x_dtype, soft, right != 0, g, p, static_cast<hipStream_t>(stream)));
 }
 
 int ace_backward(const void* x, int x_dtype, const void* target, int target_kind,
@@ -232,7 +264,6 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   p.K = num_bins;
   p.act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
   p.tk = labels ? kTgtLabels : kTgtOnehot;
-  p.right = right != 0;
   p.vec_ok = vec_ok ? 1 : 0;
   p.go_per_class = grad_output_per_class != 0;
   p.btab = bin_table;
@@ -242,21 +273,7 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   p.jac = jac;
   p.go = grad_output;
 
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  switch (x_dtype) {
-    case ACE_F32:
-      e = soft ? launch_variant_bwd<float, true>(g, p, s) : launch_variant_bwd<float, false>(g, p, s);
-      break;
-    case ACE_BF16:
-      e = soft ? launch_variant_bwd<__hip_bfloat16, true>(g, p, s)
-               : launch_variant_bwd<__hip_bfloat16, false>(g, p, s);
-      break;
-    default:
-      e = soft ? launch_variant_bwd<__half, true>(g, p, s) : launch_variant_bwd<__half, false>(g, p, s);
-      break;
-  }
-  return to_code(e);
+  return to_code(dispatch_bwd(x_dtype, soft, right != 0, g, p, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

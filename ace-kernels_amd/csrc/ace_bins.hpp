@@ -23,15 +23,19 @@ namespace ace {
 // The result is clamped to [0, n - 1]: p > 1 + eps32 and NaN are outside the
 // reference's domain (its scatter raises for them), and the clamp keeps every
 // histogram index in range.
-ACE_HD int bucket(float p, float nf, int n, const float* tab, bool right) {
-  const float t = fminf(fmaxf(p * nf, 0.0f), nf);  // fmaxf(NaN, 0) = 0
+// CLAMP = false is for probabilities known to lie in [0, 1] (softmax output):
+// p * n is then in [0, n] and needs no clamping; the final clamp stays so that
+// NaN logits cannot produce an index out of range.
+template <bool RIGHT, bool CLAMP = true>
+ACE_HD int bucket(float p, float nf, int n, const float* tab) {
+  const float t = CLAMP ? fminf(fmaxf(p * nf, 0.0f), nf) : p * nf;  // fmaxf(NaN, 0) = 0
   const int g = (int)t;                            // t >= 0: truncation is floor
   const float lo = tab[g];                         // table[g - 1]
   const float hi = tab[g + 1];                     // table[g]
-  const bool up = right ? (hi <= p) : (hi < p);
+  const bool up = RIGHT ? (hi <= p) : (hi < p);
   const int g1 = g + (up ? 1 : 0);
   const float lo1 = up ? hi : lo;                  // table[g1 - 1]
-  const bool keep = right ? (lo1 <= p) : (lo1 < p);
+  const bool keep = RIGHT ? (lo1 <= p) : (lo1 < p);
   int g2 = g1 - (keep ? 0 : 1);
   g2 = g2 < 0 ? 0 : g2;
   return g2 > n - 1 ? n - 1 : g2;

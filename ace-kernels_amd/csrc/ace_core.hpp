@@ -7,13 +7,13 @@
 // sums are fixed-point integers (30 fraction bits) added with LDS integer
 // atomics, so they are exact for the float32 terms >= 2^-7 (and within 2^-31
 // per term below) and independent of the order of addition: the result is
-// bitwise deterministic with no float atomics.  Each wave lane adds into copy
-// (lane % copies) of the histogram; with 16 copies laid out bin-major the 16
-// lanes an LDS cycle serves always hit 16 distinct bank pairs, whatever their
-// bins, so the atomics never conflict.  Blocks then write integer partials;
-// the last block of each group (ticket counter) sums its group, and the last
-// group's block sums the groups and runs the epilogue (d, coef, per-class
-// error, jac, loss).  Counters are reset by the blocks that consume them.
+// bitwise deterministic with no float atomics.  Lane l of a wave adds into
+// copy (l % copies) of the histogram, copies laid out bin-major, so the lanes
+// one LDS cycle serves hit distinct banks whatever their bins.  Each block
+// then publishes an integer partial; the last block of each group (ticket
+// counter) sums its group into the final sums with integer atomics, and the
+// last group's block runs the epilogue (d, coef, per-class error, jac, loss)
+// and leaves counters and sums zero for the next call.
 //
 // Backward (one launch): recompute the activation and the bins from the
 // logits with the same device functions (identical bits), gather coef (and d
@@ -40,6 +40,13 @@ enum { kRedMean = 0, kRedSum = 1, kRedNone = 2 };
 enum { kTgtLabels = 0, kTgtOnehot = 1 };
 enum { kReduceTree = 0, kReduceDirect = 1 };
 
+// Packed hard-binning histogram word: count | label count | sum p.
+//   bits [53, 64): voxels in the bin (<= 2047 per copy and block)
+//   bits [42, 53): voxels of the bin whose label is this channel
+//   bits [ 0, 42): sum of p in 30-bit fixed point (|sum| < 2^11)
+constexpr int kShiftN = 53;
+constexpr int kShiftG = 42;
+
 struct FwdParams {
   const void* x;
   const void* tgt;
@@ -48,7 +55,7 @@ struct FwdParams {
   int64_t tiles;
   int64_t gs;
   int64_t gpb;
-  int B, C, off, K, act, tk, right, copies, vec_ok, ignore_empty, red;
+  int B, C, off, K, act, tk, copies, vec_ok, ignore_empty, red;
   int mode;            // kReduceTree or kReduceDirect
   int epi_batch;       // batch indices per epilogue pass
   float empty_w;
@@ -73,7 +80,7 @@ struct BwdParams {
   int64_t N;
   int64_t tile_vox;
   int64_t tiles;
-  int B, C, off, K, act, tk, right, vec_ok, go_per_class;
+  int B, C, off, K, act, tk, vec_ok, go_per_class;
   const float* btab;
   const float* rtab;
   const float* coef;
@@ -133,10 +140,11 @@ __device__ __forceinline__ int label_channel(long long v, int C) {
   return (v >= 0 && v < (long long)C) ? (int)v : -1;
 }
 
+// VEC labels from an address aligned to 16 bytes (VEC even) or one label.
 template <int VEC>
 __device__ __forceinline__ void load_labels(const long long* __restrict__ p, int C,
-                                            bool aligned, int nv, int (&lab)[VEC]) {
-  if (aligned && nv == VEC && (VEC % 2) == 0) {
+                                            int (&lab)[VEC]) {
+  if constexpr (VEC % 2 == 0) {
 #pragma unroll
     for (int j = 0; j < VEC; j += 2) {
       const longlong2 t = *reinterpret_cast<const longlong2*>(p + j);
@@ -145,26 +153,48 @@ __device__ __forceinline__ void load_labels(const long long* __restrict__ p, int
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) lab[j] = j < nv ? label_channel(p[j], C) : -1;
+    for (int j = 0; j < VEC; ++j) lab[j] = label_channel(p[j], C);
   }
 }
 
+// VEC consecutive elements, vector load when VEC > 1 (caller guarantees
+// alignment) or one element.
 template <typename T, int VEC>
-__device__ __forceinline__ void load_row(const T* __restrict__ p, bool aligned, int nv,
-                                         float (&out)[VEC]) {
-  if (aligned && nv == VEC) {
+__device__ __forceinline__ void load_row(const T* __restrict__ p, float (&out)[VEC]) {
+  if constexpr (VEC > 1) {
     load_vec<T, VEC>(p, out);
   } else {
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) out[j] = j < nv ? to_f32<T>(p[j]) : 0.0f;
+    out[0] = to_f32<T>(p[0]);
   }
+}
+
+// ------------------------------------------------------------ division
+
+// Correctly rounded a / b with the reciprocal y = rcp_rn(b) shared by every
+// numerator over b: y is v_rcp_f32 refined by one Newton step, which equals the
+// IEEE quotient 1 / b for every float b in [2^-20, 2^20) (checked exhaustively
+// on MI355X); given y = RN(1 / b), two residual corrections of a * y give the
+// IEEE quotient (Markstein's theorem), checked against '/' for 2e10 (a, b)
+// pairs.  Used where b is a softmax sum in [1, C] or a soft-bin span in
+// [2^-20, 2^14]; bit-identical to '/', at a quarter of its instructions.
+__device__ __forceinline__ float rcp_rn(float b) {
+  const float y = __builtin_amdgcn_rcpf(b);
+  const float e = fmaf(-b, y, 1.0f);
+  return fmaf(e, y, y);
+}
+__device__ __forceinline__ float div_rn(float a, float b, float y) {
+  float q = a * y;
+  float r = fmaf(-b, q, a);
+  q = fmaf(r, y, q);
+  r = fmaf(-b, q, a);
+  return fmaf(r, y, q);
 }
 
 // ------------------------------------------------------------ activation
 
 // In place: logits -> probabilities.  Softmax follows torch.softmax: max over
 // channels, e_c = exp(x_c - max), s = sequential sum over c, p_c = e_c / s
-// with IEEE division (hipcc's default for '/'), and ROCm's accurate expf.
+// (IEEE quotient), with ROCm's accurate expf.  Sigmoid: 1 / (1 + exp(-x)).
 template <int CMAX, bool EXACT>
 __device__ __forceinline__ void activate(float (&x)[CMAX], int nc, int act) {
   if (act == kActSoftmax) {
@@ -179,9 +209,10 @@ __device__ __forceinline__ void activate(float (&x)[CMAX], int nc, int act) {
         x[c] = expf(x[c] - m);
         s += x[c];
       }
+    const float y = rcp_rn(s);
 #pragma unroll
     for (int c = 0; c < CMAX; ++c)
-      if (EXACT || c < nc) x[c] = x[c] / s;
+      if (EXACT || c < nc) x[c] = div_rn(x[c], s, y);
   } else if (act == kActSigmoid) {
 #pragma unroll
     for (int c = 0; c < CMAX; ++c)
@@ -193,24 +224,27 @@ __device__ __forceinline__ void activate(float (&x)[CMAX], int nc, int act) {
 
 struct SoftW {
   int l, r;
-  float lw, rw, span;
+  float lw, rw, span, inv_span;
 };
 
 // Soft assignment of common.py:43-61: half-bin index h against the 2K upper
 // half boundaries; bins l = max(h-1,0)/2, r = min(h+1,2K-1)/2; distances to
-// the replicated centres (sentinels +-1e4); lw = rd/S, rw = ld/S (IEEE).
+// the replicated centres (sentinels +-1e4); lw = rd/S, rw = ld/S and 1/S, all
+// IEEE quotients (one shared reciprocal of S).
+template <bool RIGHT, bool CLAMP = true>
 __device__ __forceinline__ SoftW soft_assign(float p, int K, float n2f, const float* htab,
-                                             const float* repl, bool right) {
+                                             const float* repl) {
   const int n2 = 2 * K;
-  const int h = bucket(p, n2f, n2, htab, right);
+  const int h = bucket<RIGHT, CLAMP>(p, n2f, n2, htab);
   SoftW w;
   w.l = max(h - 1, 0) >> 1;
   w.r = min(h + 1, n2 - 1) >> 1;
   const float ld = p - repl[h];
   const float rd = repl[h + 2] - p;
   w.span = ld + rd;
-  w.lw = rd / w.span;
-  w.rw = ld / w.span;
+  w.inv_span = rcp_rn(w.span);
+  w.lw = div_rn(rd, w.span, w.inv_span);
+  w.rw = div_rn(ld, w.span, w.inv_span);
   return w;
 }
 
@@ -223,8 +257,8 @@ __device__ __forceinline__ long long fx(float v) {
 __device__ __forceinline__ void lds_add(unsigned long long* p, unsigned long long v) {
   __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ void lds_add(unsigned int* p, unsigned int v) {
-  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+__device__ __forceinline__ void lds_add(long long* p, long long v) {
+  lds_add(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
 }
 
 // Cross-block communication without cache-wide fences.  An agent-scope
@@ -254,7 +288,7 @@ __device__ __forceinline__ int ticket(int* ctr) {
 }
 
 // Copies the bucket table (padded with -inf / +inf) and the centre table into
-// LDS; returns pointers to both.
+// LDS.
 __device__ __forceinline__ void load_tables(float* lds, const float* btab, const float* rtab,
                                             int n, int nrepl) {
   for (int i = threadIdx.x; i < n + 2; i += kThreads) {
@@ -267,140 +301,118 @@ __device__ __forceinline__ void load_tables(float* lds, const float* btab, const
   for (int i = threadIdx.x; i < nrepl; i += kThreads) lds[n + 2 + i] = rtab[i];
 }
 
-// ------------------------------------------------------------ forward
+// ------------------------------------------------------------ tiles
 
-// Sums of a voxel's contribution into histogram copy `copy`.
-//  hard: A[(c'K + k) * R + copy] += (1 << 48) + fx(p)   (count and sum p)
-//        G: labels -> u32 count at the label channel's bin;
-//           one-hot -> i64 fx(y) per channel with y != 0
-//  soft: W, P, G i64 at bins l and r.
-template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT>
-__global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  float* tabs = reinterpret_cast<float*>(smem);
-  const int K = P.K;
-  const int n = SOFT ? 2 * K : K;
-  const int nc = EXACT ? CMAX : P.C;
-  const int off = P.off;
-  const int CL = nc - off;
-  const int CK = CL * K;
-  const int R = P.copies;
-  const int tid = threadIdx.x;
-  const int64_t blk = blockIdx.x;
-  const int b = (int)(blk / P.tiles);
-  const int64_t tile = blk - (int64_t)b * P.tiles;
-  const float nf = (float)n;
-  const bool right = P.right != 0;
-  const bool labels = P.tk == kTgtLabels;
+// One thread's slice of a step: VEC voxels of every channel, their labels or
+// per-channel targets.  `load` issues the vector loads only; the values are
+// first used by the binning, so a load can be in flight while another tile is
+// processed.
+template <int CMAX, int VEC>
+struct Tile {
+  float x[CMAX][VEC];
+  int lab[VEC];
+  float y[CMAX][VEC];
 
-  const size_t tab_floats = (size_t)(((n + 2) + (SOFT ? 2 * K + 2 : 0) + 3) / 4 * 4);
-  unsigned char* hist = smem + tab_floats * 4;
-  unsigned long long* histA = reinterpret_cast<unsigned long long*>(hist);       // hard
-  unsigned int* histGc = reinterpret_cast<unsigned int*>(hist + (size_t)CK * R * 8);
-  long long* histGf = reinterpret_cast<long long*>(hist + (size_t)CK * R * 8);
-  long long* histW = reinterpret_cast<long long*>(hist);                         // soft
-  long long* histP = histW + (size_t)CK * R;
-  long long* histG = histP + (size_t)CK * R;
-  const size_t hist_words =
-      (hist_bytes_per_copy(CK, SOFT, labels) * (size_t)R + 7) / 8;
-
-  load_tables(tabs, P.btab, P.rtab, n, SOFT ? 2 * K + 2 : 0);
-  {
-    unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
-    for (size_t i = tid; i < hist_words; i += kThreads) h64[i] = 0ull;
-  }
-  __syncthreads();
-  const float* btab = tabs;
-  const float* repl = tabs + n + 2;
-  const int copy = tid & (R - 1);
-
-  const T* xb = reinterpret_cast<const T*>(P.x) + (int64_t)b * nc * P.N;
-  const long long* lb = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * P.N;
-  const float* yb = reinterpret_cast<const float*>(P.tgt) + (int64_t)b * nc * P.N;
-  const int64_t v0 = tile * P.tile_vox;
-  const int64_t v1 = min(v0 + P.tile_vox, P.N);
-  const bool aligned = P.vec_ok != 0;
-
-  for (int64_t v = v0 + (int64_t)tid * VEC; v < v1; v += (int64_t)kThreads * VEC) {
-    const int nv = (int)min((int64_t)VEC, v1 - v);
-    float xv[CMAX][VEC];
+  template <typename T, bool EXACT>
+  __device__ __forceinline__ void load(const T* xt, const long long* lt, const float* yt,
+                                       int64_t N, int v, int nc, int off, bool labels) {
 #pragma unroll
     for (int c = 0; c < CMAX; ++c)
-      if (EXACT || c < nc) load_row<T, VEC>(xb + (int64_t)c * P.N + v, aligned, nv, xv[c]);
-    int lab[VEC];
-    float yv[CMAX][VEC];
+      if (EXACT || c < nc) load_row<T, VEC>(xt + c * N + v, x[c]);
     if (labels) {
-      load_labels<VEC>(lb + v, nc, aligned, nv, lab);
+      load_labels<VEC>(lt + v, nc, lab);
     } else {
 #pragma unroll
       for (int c = 0; c < CMAX; ++c)
-        if ((EXACT || c < nc) && c >= off) load_row<float, VEC>(yb + (int64_t)c * P.N + v, aligned, nv, yv[c]);
+        if ((EXACT || c < nc) && c >= off) load_row<float, VEC>(yt + c * N + v, y[c]);
     }
+  }
+};
+
+// ------------------------------------------------------------ forward
+
+// LDS views of one block's histogram copies.
+struct Hist {
+  unsigned long long* a;  // hard: packed count | label count | sum p   [CK][R]
+  long long* g1;          // hard + per-channel targets: sum y          [CK][R]
+  long long* w;           // soft: sum of weights                       [CK][R]
+  long long* p;           // soft: sum of weight * p                    [CK][R]
+  long long* g;           // soft: sum of weight * y                    [CK][R]
+};
+
+// Adds NV voxels (logits xv, labels lab or targets yv) into the histograms.
+template <int CMAX, bool EXACT, int NV, bool SOFT, bool RIGHT>
+__device__ __forceinline__ void fwd_accumulate(const FwdParams& P, const Hist& H, const float* btab,
+                                               const float* repl, int nc, int copy,
+                                               float (&xv)[CMAX][NV], const int (&lab)[NV],
+                                               const float (&yv)[CMAX][NV], bool labels) {
+  const int K = P.K;
+  const int off = P.off;
+  const int R = P.copies;
+  const float nf = (float)(SOFT ? 2 * K : K);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      if (j >= nv) break;
-      float p[CMAX];
+  for (int j = 0; j < NV; ++j) {
+    float p[CMAX];
 #pragma unroll
-      for (int c = 0; c < CMAX; ++c) p[c] = xv[c][j];
-      activate<CMAX, EXACT>(p, nc, P.act);
-      if constexpr (!SOFT) {
-        int kl = 0;
+    for (int c = 0; c < CMAX; ++c) p[c] = xv[c][j];
+    activate<CMAX, EXACT>(p, nc, P.act);
+    if constexpr (!SOFT) {
 #pragma unroll
-        for (int c = 0; c < CMAX; ++c) {
-          if (!(EXACT || c < nc) || c < off) continue;
-          const int k = bucket(p[c], nf, n, btab, right);
-          const int slot = ((c - off) * K + k) * R + copy;
-          const unsigned long long add =
-              (1ull << 48) + (unsigned long long)fx(p[c]);
-          lds_add(&histA[slot], add);
-          if (labels) {
-            kl = (lab[j] == c) ? k : kl;
-          } else {
-            const float y = yv[c][j];
-            if (y != 0.0f) lds_add(reinterpret_cast<unsigned long long*>(&histGf[slot]),
-                                   (unsigned long long)fx(y));
+      for (int c = 0; c < CMAX; ++c) {
+        if (!(EXACT || c < nc) || c < off) continue;
+        const int k = bucket<RIGHT>(p[c], nf, K, btab);
+        const int slot = ((c - off) * K + k) * R + copy;
+        const unsigned long long hit = (labels && lab[j] == c) ? (1ull << kShiftG) : 0ull;
+        lds_add(&H.a[slot], (1ull << kShiftN) + hit + (unsigned long long)fx(p[c]));
+        if (!labels) {
+          const float y = yv[c][j];
+          if (y != 0.0f) lds_add(&H.g1[slot], fx(y));
+        }
+      }
+    } else {
+      int gl = 0, gr = 0;
+      float glw = 0.0f, grw = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CMAX; ++c) {
+        if (!(EXACT || c < nc) || c < off) continue;
+        const SoftW w = soft_assign<RIGHT>(p[c], K, nf, btab, repl);
+        const int sl = ((c - off) * K + w.l) * R + copy;
+        const int sr = ((c - off) * K + w.r) * R + copy;
+        lds_add(&H.w[sl], fx(w.lw));
+        lds_add(&H.w[sr], fx(w.rw));
+        lds_add(&H.p[sl], fx(w.lw * p[c]));
+        lds_add(&H.p[sr], fx(w.rw * p[c]));
+        if (labels) {
+          const bool hit = lab[j] == c;
+          gl = hit ? sl : gl;
+          gr = hit ? sr : gr;
+          glw = hit ? w.lw : glw;
+          grw = hit ? w.rw : grw;
+        } else {
+          const float y = yv[c][j];
+          if (y != 0.0f) {
+            lds_add(&H.g[sl], fx(w.lw * y));
+            lds_add(&H.g[sr], fx(w.rw * y));
           }
         }
-        if (labels && lab[j] >= off) {
-          const int slot = ((lab[j] - off) * K + kl) * R + copy;
-          lds_add(&histGc[slot], 1u);
-        }
-      } else {
-        int gl = 0, gr = 0;
-        float glw = 0.0f, grw = 0.0f;
-#pragma unroll
-        for (int c = 0; c < CMAX; ++c) {
-          if (!(EXACT || c < nc) || c < off) continue;
-          const SoftW w = soft_assign(p[c], K, nf, btab, repl, right);
-          const int sl = ((c - off) * K + w.l) * R + copy;
-          const int sr = ((c - off) * K + w.r) * R + copy;
-          lds_add(reinterpret_cast<unsigned long long*>(&histW[sl]), (unsigned long long)fx(w.lw));
-          lds_add(reinterpret_cast<unsigned long long*>(&histW[sr]), (unsigned long long)fx(w.rw));
-          lds_add(reinterpret_cast<unsigned long long*>(&histP[sl]), (unsigned long long)fx(w.lw * p[c]));
-          lds_add(reinterpret_cast<unsigned long long*>(&histP[sr]), (unsigned long long)fx(w.rw * p[c]));
-          if (labels) {
-            const bool hit = lab[j] == c;
-            gl = hit ? sl : gl;
-            gr = hit ? sr : gr;
-            glw = hit ? w.lw : glw;
-            grw = hit ? w.rw : grw;
-          } else {
-            const float y = yv[c][j];
-            if (y != 0.0f) {
-              lds_add(reinterpret_cast<unsigned long long*>(&histG[sl]), (unsigned long long)fx(w.lw * y));
-              lds_add(reinterpret_cast<unsigned long long*>(&histG[sr]), (unsigned long long)fx(w.rw * y));
-            }
-          }
-        }
-        if (labels && lab[j] >= off) {
-          lds_add(reinterpret_cast<unsigned long long*>(&histG[gl]), (unsigned long long)fx(glw));
-          lds_add(reinterpret_cast<unsigned long long*>(&histG[gr]), (unsigned long long)fx(grw));
-        }
+      }
+      if (labels && lab[j] >= off) {
+        lds_add(&H.g[gl], fx(glw));
+        lds_add(&H.g[gr], fx(grw));
       }
     }
   }
-  __syncthreads();
+}
 
+// ---- end of a forward block: publish the block's sums, and in the last
+// block of a group / of the grid run the reductions and the epilogue
+template <bool SOFT>
+__device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, unsigned char* hist,
+                                           int CK, int CL, int b, int64_t tile, int64_t blk,
+                                           bool labels) {
+  const int tid = threadIdx.x;
+  const int K = P.K;
+  const int R = P.copies;
   // ---- block partial: sum the copies -> W3 = 3 x CK fixed-point values
   const int W3 = 3 * CK;
   const bool direct = P.mode == kReduceDirect;
@@ -409,17 +421,19 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
   for (int t = tid; t < CK; t += kThreads) {
     long long s0 = 0, s1 = 0, s2 = 0;
     for (int r = 0; r < R; ++r) {
-      const int slot = t * R + r;
+      // skew the copy index by t: neighbouring threads read neighbouring banks
+      const int slot = t * R + ((r + t) & (R - 1));
       if constexpr (!SOFT) {
-        const unsigned long long a = histA[slot];
-        const unsigned long long cnt = (a + (1ull << 47)) >> 48;
-        s0 += (long long)(cnt << kFrac);
-        s1 += (long long)(a - (cnt << 48));
-        s2 += labels ? ((long long)histGc[slot] << kFrac) : histGf[slot];
+        const unsigned long long a = H.a[slot];
+        const unsigned long long hi = (a + (1ull << (kShiftG - 1))) >> kShiftG;
+        s0 += (long long)((hi >> (kShiftN - kShiftG)) << kFrac);
+        s1 += (long long)(a - (hi << kShiftG));
+        s2 += labels ? (long long)((hi & ((1ull << (kShiftN - kShiftG)) - 1)) << kFrac)
+                     : H.g1[slot];
       } else {
-        s0 += histW[slot];
-        s1 += histP[slot];
-        s2 += histG[slot];
+        s0 += H.w[slot];
+        s1 += H.p[slot];
+        s2 += H.g[slot];
       }
     }
     if (direct) {
@@ -572,9 +586,156 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
   }
 }
 
+template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
+__global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* tabs = reinterpret_cast<float*>(smem);
+  const int K = P.K;
+  const int n = SOFT ? 2 * K : K;
+  const int nc = EXACT ? CMAX : P.C;
+  const int off = P.off;
+  const int CL = nc - off;
+  const int CK = CL * K;
+  const int R = P.copies;
+  const int tid = threadIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int b = (int)(blk / P.tiles);
+  const int64_t tile = blk - (int64_t)b * P.tiles;
+  const bool labels = P.tk == kTgtLabels;
+
+  const size_t tab_floats = (size_t)(((n + 2) + (SOFT ? 2 * K + 2 : 0) + 3) / 4 * 4);
+  unsigned char* hist = smem + tab_floats * 4;
+  Hist H;
+  H.a = reinterpret_cast<unsigned long long*>(hist);
+  H.g1 = reinterpret_cast<long long*>(hist) + (size_t)CK * R;
+  H.w = reinterpret_cast<long long*>(hist);
+  H.p = H.w + (size_t)CK * R;
+  H.g = H.p + (size_t)CK * R;
+  const size_t hist_words = (hist_bytes_per_copy(CK, SOFT, labels) * (size_t)R + 7) / 8;
+
+  load_tables(tabs, P.btab, P.rtab, n, SOFT ? 2 * K + 2 : 0);
+  {
+    unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
+    for (size_t i = tid; i < hist_words; i += kThreads) h64[i] = 0ull;
+  }
+  __syncthreads();
+  const float* btab = tabs;
+  const float* repl = tabs + n + 2;
+  const int copy = tid & (R - 1);
+
+  // this tile: voxels [t0, t0 + nvox) of batch index b
+  const int64_t N = P.N;
+  const int64_t t0 = tile * P.tile_vox;
+  const int nvox = (int)min(P.tile_vox, N - t0);
+  const T* xt = reinterpret_cast<const T*>(P.x) + (int64_t)b * nc * N + t0;
+  const long long* lt = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
+  const float* yt = reinterpret_cast<const float*>(P.tgt) + (int64_t)b * nc * N + t0;
+  const int nfull = P.vec_ok ? nvox / VEC * VEC : 0;
+
+  // full vector steps, software-pipelined: the next step's loads are in flight
+  // while the current step is binned (two buffers, unrolled by two)
+  {
+    Tile<CMAX, VEC> ta, tb;
+    const int stride = kThreads * VEC;
+    int v = tid * VEC;
+    if (v < nfull) ta.template load<T, EXACT>(xt, lt, yt, N, v, nc, off, labels);
+    for (; v < nfull; v += 2 * stride) {
+      if (v + stride < nfull) tb.template load<T, EXACT>(xt, lt, yt, N, v + stride, nc, off, labels);
+      fwd_accumulate<CMAX, EXACT, VEC, SOFT, RIGHT>(P, H, btab, repl, nc, copy, ta.x, ta.lab, ta.y, labels);
+      if (v + 2 * stride < nfull) ta.template load<T, EXACT>(xt, lt, yt, N, v + 2 * stride, nc, off, labels);
+      if (v + stride < nfull)
+        fwd_accumulate<CMAX, EXACT, VEC, SOFT, RIGHT>(P, H, btab, repl, nc, copy, tb.x, tb.lab, tb.y, labels);
+    }
+  }
+  for (int v = nfull + tid; v < nvox; v += kThreads) {
+    float xv[CMAX][1];
+#pragma unroll
+    for (int c = 0; c < CMAX; ++c)
+      if (EXACT || c < nc) load_row<T, 1>(xt + c * N + v, xv[c]);
+    int lab[1];
+    float yv[CMAX][1];
+    if (labels) {
+      load_labels<1>(lt + v, nc, lab);
+    } else {
+#pragma unroll
+      for (int c = 0; c < CMAX; ++c)
+        if ((EXACT || c < nc) && c >= off) load_row<float, 1>(yt + c * N + v, yv[c]);
+    }
+    fwd_accumulate<CMAX, EXACT, 1, SOFT, RIGHT>(P, H, btab, repl, nc, copy, xv, lab, yv, labels);
+  }
+  __syncthreads();
+  fwd_finish<SOFT>(P, H, hist, CK, CL, b, tile, blk, labels);
+}
+
 // ------------------------------------------------------------ backward
 
-template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT>
+// dL/dx of NV voxels, in place in xv (logits in, gradient out).
+template <int CMAX, bool EXACT, int NV, bool SOFT, bool RIGHT>
+__device__ __forceinline__ void bwd_voxels(const BwdParams& P, const float* btab, const float* repl,
+                                           const float* scoef, const float* sdd, const float* sg,
+                                           int nc, float (&xv)[CMAX][NV], const int (&lab)[NV],
+                                           const float (&yv)[CMAX][NV], bool labels) {
+  const int K = P.K;
+  const int off = P.off;
+  const float nf = (float)(SOFT ? 2 * K : K);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    float p[CMAX];
+#pragma unroll
+    for (int c = 0; c < CMAX; ++c) p[c] = xv[c][j];
+    activate<CMAX, EXACT>(p, nc, P.act);
+    float gp[CMAX];
+#pragma unroll
+    for (int c = 0; c < CMAX; ++c) {
+      gp[c] = 0.0f;
+      if (!(EXACT || c < nc) || c < off) continue;
+      const int cl = c - off;
+      if constexpr (!SOFT) {
+        const int k = bucket<RIGHT>(p[c], nf, K, btab);
+        gp[c] = scoef[cl * K + k] * sg[cl];
+      } else {
+        const SoftW w = soft_assign<RIGHT>(p[c], K, nf, btab, repl);
+        const float y = labels ? (lab[j] == c ? 1.0f : 0.0f) : yv[c][j];
+        const float resid = p[c] - y;
+        const float left = scoef[cl * K + w.l] * (w.lw - w.inv_span * (resid - sdd[cl * K + w.l]));
+        const float rght = scoef[cl * K + w.r] * (w.rw + w.inv_span * (resid - sdd[cl * K + w.r]));
+        gp[c] = sg[cl] * (left + rght);
+      }
+    }
+    if (P.act == kActSoftmax) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CMAX; ++c)
+        if (EXACT || c < nc) dot += gp[c] * p[c];
+#pragma unroll
+      for (int c = 0; c < CMAX; ++c)
+        if (EXACT || c < nc) xv[c][j] = p[c] * (gp[c] - dot);
+    } else if (P.act == kActSigmoid) {
+#pragma unroll
+      for (int c = 0; c < CMAX; ++c)
+        if (EXACT || c < nc) xv[c][j] = gp[c] * p[c] * (1.0f - p[c]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < CMAX; ++c)
+        if (EXACT || c < nc) xv[c][j] = gp[c];
+    }
+  }
+}
+
+template <typename T, bool EXACT, int CMAX, int VEC>
+__device__ __forceinline__ void bwd_load(Tile<CMAX, VEC>& t, const T* xt, const long long* lt,
+                                         const float* yt, int64_t N, int v, int nc, int off,
+                                         bool labels, bool need_tgt) {
+  if (need_tgt) {
+    t.template load<T, EXACT>(xt, lt, yt, N, v, nc, off, labels);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CMAX; ++c)
+      if (EXACT || c < nc) load_row<T, VEC>(xt + c * N + v, t.x[c]);
+  }
+}
+
+template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
 __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* tabs = reinterpret_cast<float*>(smem);
@@ -588,8 +749,6 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
   const int64_t blk = blockIdx.x;
   const int b = (int)(blk / P.tiles);
   const int64_t tile = blk - (int64_t)b * P.tiles;
-  const float nf = (float)n;
-  const bool right = P.right != 0;
   const bool labels = P.tk == kTgtLabels;
 
   const size_t tab_floats = (size_t)(((n + 2) + (SOFT ? 2 * K + 2 : 0) + 3) / 4 * 4);
@@ -609,99 +768,403 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
   const float* btab = tabs;
   const float* repl = tabs + n + 2;
 
-  const T* xb = reinterpret_cast<const T*>(P.x) + (int64_t)b * nc * P.N;
-  T* db = reinterpret_cast<T*>(P.dx) + (int64_t)b * nc * P.N;
-  const long long* lb = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * P.N;
-  const float* yb = reinterpret_cast<const float*>(P.tgt) + (int64_t)b * nc * P.N;
-  const int64_t v0 = tile * P.tile_vox;
-  const int64_t v1 = min(v0 + P.tile_vox, P.N);
-  const bool aligned = P.vec_ok != 0;
+  const int64_t N = P.N;
+  const int64_t t0 = tile * P.tile_vox;
+  const int nvox = (int)min(P.tile_vox, N - t0);
+  const T* xt = reinterpret_cast<const T*>(P.x) + (int64_t)b * nc * N + t0;
+  T* dt = reinterpret_cast<T*>(P.dx) + (int64_t)b * nc * N + t0;
+  const long long* lt = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
+  const float* yt = reinterpret_cast<const float*>(P.tgt) + (int64_t)b * nc * N + t0;
+  const int nfull = P.vec_ok ? nvox / VEC * VEC : 0;
 
-  for (int64_t v = v0 + (int64_t)tid * VEC; v < v1; v += (int64_t)kThreads * VEC) {
-    const int nv = (int)min((int64_t)VEC, v1 - v);
-    float xv[CMAX][VEC];
+  // full vector steps, software-pipelined as in the forward
+  {
+    Tile<CMAX, VEC> ta, tb;
+    const int stride = kThreads * VEC;
+    // the hard gradient needs no targets: only the logits are loaded
+    const bool need_tgt = SOFT;
+    int v = tid * VEC;
+    if (v < nfull) bwd_load<T, EXACT, CMAX, VEC>(ta, xt, lt, yt, N, v, nc, off, labels, need_tgt);
+    for (; v < nfull; v += 2 * stride) {
+      if (v + stride < nfull)
+        bwd_load<T, EXACT, CMAX, VEC>(tb, xt, lt, yt, N, v + stride, nc, off, labels, need_tgt);
+      bwd_voxels<CMAX, EXACT, VEC, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sg, nc, ta.x, ta.lab, ta.y, labels);
+#pragma unroll
+      for (int c = 0; c < CMAX; ++c)
+        if (EXACT || c < nc) store_vec<T, VEC>(dt + c * N + v, ta.x[c]);
+      if (v + 2 * stride < nfull)
+        bwd_load<T, EXACT, CMAX, VEC>(ta, xt, lt, yt, N, v + 2 * stride, nc, off, labels, need_tgt);
+      if (v + stride < nfull) {
+        bwd_voxels<CMAX, EXACT, VEC, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sg, nc, tb.x, tb.lab, tb.y, labels);
+#pragma unroll
+        for (int c = 0; c < CMAX; ++c)
+          if (EXACT || c < nc) store_vec<T, VEC>(dt + c * N + v + stride, tb.x[c]);
+      }
+    }
+  }
+  for (int v = nfull + tid; v < nvox; v += kThreads) {
+    float xv[CMAX][1];
 #pragma unroll
     for (int c = 0; c < CMAX; ++c)
-      if (EXACT || c < nc) load_row<T, VEC>(xb + (int64_t)c * P.N + v, aligned, nv, xv[c]);
-    int lab[VEC];
-    float yv[CMAX][VEC];
+      if (EXACT || c < nc) load_row<T, 1>(xt + c * N + v, xv[c]);
+    int lab[1];
+    float yv[CMAX][1];
     if (SOFT) {
       if (labels) {
-        load_labels<VEC>(lb + v, nc, aligned, nv, lab);
+        load_labels<1>(lt + v, nc, lab);
       } else {
 #pragma unroll
         for (int c = 0; c < CMAX; ++c)
-          if ((EXACT || c < nc) && c >= off) load_row<float, VEC>(yb + (int64_t)c * P.N + v, aligned, nv, yv[c]);
+          if ((EXACT || c < nc) && c >= off) load_row<float, 1>(yt + c * N + v, yv[c]);
       }
     }
+    bwd_voxels<CMAX, EXACT, 1, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sg, nc, xv, lab, yv, labels);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      float p[CMAX];
+    for (int c = 0; c < CMAX; ++c)
+      if (EXACT || c < nc) dt[c * N + v] = from_f32<T>(xv[c][0]);
+  }
+}
+
+
+// ------------------------------------------------------------ fast path
+//
+// The benchmark configuration of the loss -- softmax over C channels with
+// class-index targets -- as kernels with no runtime switches in the voxel
+// loop.  Loads are issued unconditionally (past the last step they re-read the
+// current step, a cache hit), so the compiler can wait for exactly one
+// buffer's loads while the other buffer's are in flight.  Softmax outputs lie
+// in [0, 1], so the bin index needs no float clamp and the fixed-point terms
+// are non-negative.
+
+template <int C, int VEC>
+struct FastTile {
+  float x[C][VEC];
+  long long lab[VEC];  // raw int64 labels, converted when used
+};
+
+template <typename T, int C, int VEC>
+__device__ __forceinline__ void fast_load(FastTile<C, VEC>& t, const T* const (&xr)[C],
+                                          const long long* lr, uint32_t v, bool with_labels) {
 #pragma unroll
-      for (int c = 0; c < CMAX; ++c) p[c] = xv[c][j];
-      activate<CMAX, EXACT>(p, nc, P.act);
-      float gp[CMAX];
+  for (int c = 0; c < C; ++c) load_vec<T, VEC>(xr[c] + v, t.x[c]);
+  if (with_labels) {
+    if constexpr (VEC % 2 == 0) {
 #pragma unroll
-      for (int c = 0; c < CMAX; ++c) {
-        gp[c] = 0.0f;
-        if (!(EXACT || c < nc) || c < off) continue;
-        const int cl = c - off;
-        if constexpr (!SOFT) {
-          const int k = bucket(p[c], nf, n, btab, right);
-          gp[c] = scoef[cl * K + k] * sg[cl];
-        } else {
-          const SoftW w = soft_assign(p[c], K, nf, btab, repl, right);
-          const float y = labels ? (lab[j] == c ? 1.0f : 0.0f) : yv[c][j];
-          const float inv = 1.0f / w.span;
-          const float resid = p[c] - y;
-          const float left = scoef[cl * K + w.l] * (w.lw - inv * (resid - sdd[cl * K + w.l]));
-          const float rght = scoef[cl * K + w.r] * (w.rw + inv * (resid - sdd[cl * K + w.r]));
-          gp[c] = sg[cl] * (left + rght);
-        }
+      for (int j = 0; j < VEC; j += 2) {
+        const longlong2 q = *reinterpret_cast<const longlong2*>(lr + v + j);
+        t.lab[j] = q.x;
+        t.lab[j + 1] = q.y;
       }
-      if (P.act == kActSoftmax) {
-        float dot = 0.0f;
+    } else {
 #pragma unroll
-        for (int c = 0; c < CMAX; ++c)
-          if (EXACT || c < nc) dot += gp[c] * p[c];
-#pragma unroll
-        for (int c = 0; c < CMAX; ++c)
-          if (EXACT || c < nc) xv[c][j] = p[c] * (gp[c] - dot);
-      } else if (P.act == kActSigmoid) {
-#pragma unroll
-        for (int c = 0; c < CMAX; ++c)
-          if (EXACT || c < nc) xv[c][j] = gp[c] * p[c] * (1.0f - p[c]);
-      } else {
-#pragma unroll
-        for (int c = 0; c < CMAX; ++c)
-          if (EXACT || c < nc) xv[c][j] = gp[c];
-      }
+      for (int j = 0; j < VEC; ++j) t.lab[j] = lr[v + j];
     }
+  }
+}
+
+// Channel index of a raw label, or 0xffffffff when it names no channel.
+template <int C>
+__device__ __forceinline__ uint32_t fast_label(long long v) {
+  const uint32_t lo = (uint32_t)(unsigned long long)v;
+  const uint32_t hi = (uint32_t)((unsigned long long)v >> 32);
+  return (hi == 0u && lo < (uint32_t)C) ? lo : 0xffffffffu;
+}
+
+template <int C>
+__device__ __forceinline__ void softmax_fast(float (&x)[C]) {
+  float m = x[0];
 #pragma unroll
-    for (int c = 0; c < CMAX; ++c) {
-      if (!(EXACT || c < nc)) continue;
-      T* dst = db + (int64_t)c * P.N + v;
-      if (aligned && nv == VEC) {
-        store_vec<T, VEC>(dst, xv[c]);
-      } else {
+  for (int c = 1; c < C; ++c) m = fmaxf(m, x[c]);
+  float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < VEC; ++j)
-          if (j < nv) dst[j] = from_f32<T>(xv[c][j]);
+  for (int c = 0; c < C; ++c) {
+    x[c] = expf(x[c] - m);
+    s += x[c];
+  }
+  const float y = rcp_rn(s);
+#pragma unroll
+  for (int c = 0; c < C; ++c) x[c] = div_rn(x[c], s, y);
+}
+
+// One tile into the histogram copies.  hb[c]: this lane's copy of channel c's
+// bin 0 (u64 words), bins `R` words apart (R = 1 << lr).
+template <int C, int VEC, bool SOFT, bool RIGHT>
+__device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const float* tab,
+                                                const float* repl, int K, int off, int lr,
+                                                unsigned long long* const (&hb)[C],
+                                                const size_t words) {
+  const float nf = (float)(SOFT ? 2 * K : K);
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    float p[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) p[c] = t.x[c][j];
+    softmax_fast<C>(p);
+    const uint32_t lab = fast_label<C>(t.lab[j]);
+    if constexpr (!SOFT) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (c < off) continue;
+        const int k = bucket<RIGHT, false>(p[c], nf, K, tab);
+        const uint32_t q = (uint32_t)rintf(p[c] * 1073741824.0f);
+        const uint32_t hi = (lab == (uint32_t)c) ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
+                                                 : (1u << (kShiftN - 32));
+        lds_add(hb[c] + ((size_t)k << lr), ((unsigned long long)hi << 32) | q);
+      }
+    } else {
+      unsigned long long* gl = hb[0];
+      unsigned long long* gr = hb[0];
+      uint32_t glw = 0u, grw = 0u;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (c < off) continue;
+        const SoftW w = soft_assign<RIGHT, false>(p[c], K, nf, tab, repl);
+        unsigned long long* sl = hb[c] + ((size_t)w.l << lr);
+        unsigned long long* sr = hb[c] + ((size_t)w.r << lr);
+        const uint32_t ql = (uint32_t)rintf(w.lw * 1073741824.0f);
+        const uint32_t qr = (uint32_t)rintf(w.rw * 1073741824.0f);
+        lds_add(sl, (unsigned long long)ql);
+        lds_add(sr, (unsigned long long)qr);
+        lds_add(sl + words, (unsigned long long)(uint32_t)rintf((w.lw * p[c]) * 1073741824.0f));
+        lds_add(sr + words, (unsigned long long)(uint32_t)rintf((w.rw * p[c]) * 1073741824.0f));
+        const bool hit = lab == (uint32_t)c;
+        gl = hit ? sl : gl;
+        gr = hit ? sr : gr;
+        glw = hit ? ql : glw;
+        grw = hit ? qr : grw;
+      }
+      if (lab != 0xffffffffu && lab >= (uint32_t)off) {
+        lds_add(gl + 2 * words, (unsigned long long)glw);
+        lds_add(gr + 2 * words, (unsigned long long)grw);
       }
     }
   }
 }
 
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT>
+__global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* tabs = reinterpret_cast<float*>(smem);
+  const int K = P.K;
+  const int n = SOFT ? 2 * K : K;
+  const int off = P.off;
+  const int CL = C - off;
+  const int CK = CL * K;
+  const int R = P.copies;
+  const int lr = __builtin_ctz((unsigned)R);
+  const int tid = threadIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int b = (int)(blk / P.tiles);
+  const int64_t tile = blk - (int64_t)b * P.tiles;
+
+  const size_t tab_floats = (size_t)(((n + 2) + (SOFT ? 2 * K + 2 : 0) + 3) / 4 * 4);
+  unsigned char* hist = smem + tab_floats * 4;
+  Hist H;
+  H.a = reinterpret_cast<unsigned long long*>(hist);
+  H.g1 = reinterpret_cast<long long*>(hist) + (size_t)CK * R;
+  H.w = reinterpret_cast<long long*>(hist);
+  H.p = H.w + (size_t)CK * R;
+  H.g = H.p + (size_t)CK * R;
+  const size_t hist_words = (hist_bytes_per_copy(CK, SOFT, true) * (size_t)R + 7) / 8;
+  load_tables(tabs, P.btab, P.rtab, n, SOFT ? 2 * K + 2 : 0);
+  {
+    unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
+    for (size_t i = tid; i < hist_words; i += kThreads) h64[i] = 0ull;
+  }
+  __syncthreads();
+  const float* tab = tabs;
+  const float* repl = tabs + n + 2;
+  const int copy = tid & (R - 1);
+  unsigned long long* hb[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    hb[c] = H.a + ((size_t)((c < off ? 0 : c - off) * K) << lr) + copy;
+
+  const int64_t N = P.N;
+  const int64_t t0 = tile * P.tile_vox;
+  const int nvox = (int)min(P.tile_vox, N - t0);
+  const T* xr[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    xr[c] = reinterpret_cast<const T*>(P.x) + ((int64_t)b * C + c) * N + t0;
+  const long long* lr_ = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
+  const size_t words = (size_t)CK * R;
+  const int nfull = P.vec_ok ? nvox / VEC * VEC : 0;
+  const int stride = kThreads * VEC;
+  const int nsteps = nfull / stride;  // steps in which every thread has a full vector
+
+  if (nsteps > 0) {
+    FastTile<C, VEC> ta, tb;
+    const uint32_t v0 = (uint32_t)(tid * VEC);
+    fast_load<T, C, VEC>(ta, xr, lr_, v0, true);
+    for (int i = 0; i < nsteps; i += 2) {
+      const uint32_t va = v0 + (uint32_t)(i * stride);
+      const uint32_t vb = (i + 1 < nsteps) ? va + (uint32_t)stride : va;
+      fast_load<T, C, VEC>(tb, xr, lr_, vb, true);
+      fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, off, lr, hb, words);
+      const uint32_t vc = (i + 2 < nsteps) ? va + 2u * (uint32_t)stride : vb;
+      fast_load<T, C, VEC>(ta, xr, lr_, vc, true);
+      if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, off, lr, hb, words);
+    }
+  }
+  // remaining full vectors (not every thread has one), then single voxels
+  for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
+    FastTile<C, VEC> t;
+    fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, true);
+    fast_accumulate<C, VEC, SOFT, RIGHT>(t, tab, repl, K, off, lr, hb, words);
+  }
+  for (int v = nfull + tid; v < nvox; v += kThreads) {
+    FastTile<C, 1> t;
+    fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, true);
+    fast_accumulate<C, 1, SOFT, RIGHT>(t, tab, repl, K, off, lr, hb, words);
+  }
+  __syncthreads();
+  fwd_finish<SOFT>(P, H, hist, CK, CL, b, tile, blk, true);
+}
+
+// Backward of one tile, in place in t.x (logits in, gradient out).
+template <int C, int VEC, bool SOFT, bool RIGHT>
+__device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* tab,
+                                              const float* repl, const float* scoef,
+                                              const float* sdd, const float* sg, int K,
+                                              int off) {
+  const float nf = (float)(SOFT ? 2 * K : K);
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    float p[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) p[c] = t.x[c][j];
+    softmax_fast<C>(p);
+    float gp[C];
+    uint32_t lab = 0xffffffffu;
+    if constexpr (SOFT) lab = fast_label<C>(t.lab[j]);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      gp[c] = 0.0f;
+      if (c < off) continue;
+      const int cl = c - off;
+      if constexpr (!SOFT) {
+        const int k = bucket<RIGHT, false>(p[c], nf, K, tab);
+        gp[c] = scoef[cl * K + k] * sg[cl];
+      } else {
+        const SoftW w = soft_assign<RIGHT, false>(p[c], K, nf, tab, repl);
+        const float y = lab == (uint32_t)c ? 1.0f : 0.0f;
+        const float resid = p[c] - y;
+        const float left = scoef[cl * K + w.l] * (w.lw - w.inv_span * (resid - sdd[cl * K + w.l]));
+        const float rght = scoef[cl * K + w.r] * (w.rw + w.inv_span * (resid - sdd[cl * K + w.r]));
+        gp[c] = sg[cl] * (left + rght);
+      }
+    }
+    float dot = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) dot += gp[c] * p[c];
+#pragma unroll
+    for (int c = 0; c < C; ++c) t.x[c][j] = p[c] * (gp[c] - dot);
+  }
+}
+
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT>
+__global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* tabs = reinterpret_cast<float*>(smem);
+  const int K = P.K;
+  const int n = SOFT ? 2 * K : K;
+  const int off = P.off;
+  const int CL = C - off;
+  const int CK = CL * K;
+  const int tid = threadIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int b = (int)(blk / P.tiles);
+  const int64_t tile = blk - (int64_t)b * P.tiles;
+
+  const size_t tab_floats = (size_t)(((n + 2) + (SOFT ? 2 * K + 2 : 0) + 3) / 4 * 4);
+  float* scoef = tabs + tab_floats;
+  float* sdd = scoef + CK;
+  float* sg = sdd + (SOFT ? CK : 0);
+  load_tables(tabs, P.btab, P.rtab, n, SOFT ? 2 * K + 2 : 0);
+  for (int i = tid; i < CK; i += kThreads) {
+    scoef[i] = P.coef[(int64_t)b * CK + i];
+    if (SOFT) sdd[i] = P.d[(int64_t)b * CK + i];
+  }
+  for (int i = tid; i < CL; i += kThreads) {
+    const float go = P.go_per_class ? P.go[b * CL + i] : P.go[0];
+    sg[i] = P.jac[b * CL + i] * go;
+  }
+  __syncthreads();
+  const float* tab = tabs;
+  const float* repl = tabs + n + 2;
+
+  const int64_t N = P.N;
+  const int64_t t0 = tile * P.tile_vox;
+  const int nvox = (int)min(P.tile_vox, N - t0);
+  const T* xr[C];
+  T* dr[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    xr[c] = reinterpret_cast<const T*>(P.x) + ((int64_t)b * C + c) * N + t0;
+    dr[c] = reinterpret_cast<T*>(P.dx) + ((int64_t)b * C + c) * N + t0;
+  }
+  const long long* lr_ = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
+  const int nfull = P.vec_ok ? nvox / VEC * VEC : 0;
+  const int stride = kThreads * VEC;
+  const int nsteps = nfull / stride;
+
+  if (nsteps > 0) {
+    FastTile<C, VEC> ta, tb;
+    const uint32_t v0 = (uint32_t)(tid * VEC);
+    fast_load<T, C, VEC>(ta, xr, lr_, v0, SOFT);
+    for (int i = 0; i < nsteps; i += 2) {
+      const uint32_t va = v0 + (uint32_t)(i * stride);
+      const uint32_t vb = (i + 1 < nsteps) ? va + (uint32_t)stride : va;
+      fast_load<T, C, VEC>(tb, xr, lr_, vb, SOFT);
+      fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, repl, scoef, sdd, sg, K, off);
+#pragma unroll
+      for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + va, ta.x[c]);
+      const uint32_t vc = (i + 2 < nsteps) ? va + 2u * (uint32_t)stride : vb;
+      fast_load<T, C, VEC>(ta, xr, lr_, vc, SOFT);
+      if (i + 1 < nsteps) {
+        fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, repl, scoef, sdd, sg, K, off);
+#pragma unroll
+        for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + vb, tb.x[c]);
+      }
+    }
+  }
+  for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
+    FastTile<C, VEC> t;
+    fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, SOFT);
+    fast_backward<C, VEC, SOFT, RIGHT>(t, tab, repl, scoef, sdd, sg, K, off);
+#pragma unroll
+    for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + v, t.x[c]);
+  }
+  for (int v = nfull + tid; v < nvox; v += kThreads) {
+    FastTile<C, 1> t;
+    fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, SOFT);
+    fast_backward<C, 1, SOFT, RIGHT>(t, tab, repl, scoef, sdd, sg, K, off);
+#pragma unroll
+    for (int c = 0; c < C; ++c) dr[c][v] = from_f32<T>(t.x[c][0]);
+  }
+}
+
 // ------------------------------------------------------------ launchers
 
-template <typename T, bool SOFT>
+template <typename T, bool SOFT, bool RIGHT>
 hipError_t launch_variant_fwd(const Geometry& g, const FwdParams& prm, hipStream_t s);
-template <typename T, bool SOFT>
+template <typename T, bool SOFT, bool RIGHT>
 hipError_t launch_variant_bwd(const Geometry& g, const BwdParams& prm, hipStream_t s);
 
-template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT>
+// The fast kernels serve softmax with class-index targets for C in {2, 3, 4, 16}.
+template <int CMAX, bool EXACT>
+constexpr bool has_fast() {
+  return EXACT && (CMAX == 2 || CMAX == 3 || CMAX == 4 || CMAX == 16);
+}
+
+template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) {
-  auto kern = fwd_kernel<T, CMAX, EXACT, VEC, SOFT>;
+  auto kern = fwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
+  if constexpr (has_fast<CMAX, EXACT>()) {
+    if (prm.act == kActSoftmax && prm.tk == kTgtLabels)
+      kern = fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT>;
+  }
   if (g.lds_fwd > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -712,9 +1175,14 @@ hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) 
   return hipGetLastError();
 }
 
-template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT>
+template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) {
-  auto kern = bwd_kernel<T, CMAX, EXACT, VEC, SOFT>;
+  auto kern = bwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
+  if constexpr (has_fast<CMAX, EXACT>()) {
+    // the hard gradient reads no targets: any target layout takes the fast path
+    if (prm.act == kActSoftmax && (!SOFT || prm.tk == kTgtLabels))
+      kern = bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT>;
+  }
   if (g.lds_bwd > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -725,51 +1193,37 @@ hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) 
   return hipGetLastError();
 }
 
-// Instantiates the per-variant switch for one (element type, binning).
-#define ACE_DEFINE_LAUNCHERS(T, SOFT)                                                  \
-  template <>                                                                        \
-  hipError_t launch_variant_fwd<T, SOFT>(const Geometry& g, const FwdParams& p,      \
-                                         hipStream_t s) {                            \
-    const Variant v = g.var;                                                         \
-    if (v.exact) {                                                                   \
-      switch (v.cmax) {                                                              \
-        case 1: return launch_fwd_t<T, 1, true, 4, SOFT>(g, p, s);                   \
-        case 2: return launch_fwd_t<T, 2, true, 4, SOFT>(g, p, s);                   \
-        case 3: return launch_fwd_t<T, 3, true, 4, SOFT>(g, p, s);                   \
-        case 4: return launch_fwd_t<T, 4, true, 4, SOFT>(g, p, s);                   \
-        case 16: return launch_fwd_t<T, 16, true, 4, SOFT>(g, p, s);                 \
-      }                                                                              \
-    } else {                                                                         \
-      switch (v.cmax) {                                                              \
-        case 8: return launch_fwd_t<T, 8, false, 4, SOFT>(g, p, s);                  \
-        case 16: return launch_fwd_t<T, 16, false, 4, SOFT>(g, p, s);                \
-        case 32: return launch_fwd_t<T, 32, false, 1, SOFT>(g, p, s);                \
-        case 64: return launch_fwd_t<T, 64, false, 1, SOFT>(g, p, s);                \
-      }                                                                              \
+// Instantiates the per-variant switch for one (element type, binning, right).
+#define ACE_VARIANT_SWITCH(LAUNCH, T, SOFT, RIGHT)                                   \
+  const Variant v = g.var;                                                           \
+  if (v.exact) {                                                                     \
+    switch (v.cmax) {                                                                \
+      case 1: return LAUNCH<T, 1, true, 4, SOFT, RIGHT>(g, p, s);                    \
+      case 2: return LAUNCH<T, 2, true, 4, SOFT, RIGHT>(g, p, s);                    \
+      case 3: return LAUNCH<T, 3, true, 4, SOFT, RIGHT>(g, p, s);                    \
+      case 4: return LAUNCH<T, 4, true, 4, SOFT, RIGHT>(g, p, s);                    \
+      case 16: return LAUNCH<T, 16, true, 2, SOFT, RIGHT>(g, p, s);                  \
     }                                                                                \
-    return hipErrorInvalidValue;                                                     \
+  } else {                                                                           \
+    switch (v.cmax) {                                                                \
+      case 8: return LAUNCH<T, 8, false, 4, SOFT, RIGHT>(g, p, s);                   \
+      case 16: return LAUNCH<T, 16, false, 4, SOFT, RIGHT>(g, p, s);                 \
+      case 32: return LAUNCH<T, 32, false, 1, SOFT, RIGHT>(g, p, s);                 \
+      case 64: return LAUNCH<T, 64, false, 1, SOFT, RIGHT>(g, p, s);                 \
+    }                                                                                \
+  }                                                                                  \
+  return hipErrorInvalidValue;
+
+#define ACE_DEFINE_LAUNCHERS(T, SOFT, RIGHT)                                          \
+  template <>                                                                        \
+  hipError_t launch_variant_fwd<T, SOFT, RIGHT>(const Geometry& g, const FwdParams& p, \
+                                                hipStream_t s) {                     \
+    ACE_VARIANT_SWITCH(launch_fwd_t, T, SOFT, RIGHT)                                 \
   }                                                                                  \
   template <>                                                                        \
-  hipError_t launch_variant_bwd<T, SOFT>(const Geometry& g, const BwdParams& p,      \
-                                         hipStream_t s) {                            \
-    const Variant v = g.var;                                                         \
-    if (v.exact) {                                                                   \
-      switch (v.cmax) {                                                              \
-        case 1: return launch_bwd_t<T, 1, true, 4, SOFT>(g, p, s);                   \
-        case 2: return launch_bwd_t<T, 2, true, 4, SOFT>(g, p, s);                   \
-        case 3: return launch_bwd_t<T, 3, true, 4, SOFT>(g, p, s);                   \
-        case 4: return launch_bwd_t<T, 4, true, 4, SOFT>(g, p, s);                   \
-        case 16: return launch_bwd_t<T, 16, true, 4, SOFT>(g, p, s);                 \
-      }                                                                              \
-    } else {                                                                         \
-      switch (v.cmax) {                                                              \
-        case 8: return launch_bwd_t<T, 8, false, 4, SOFT>(g, p, s);                  \
-        case 16: return launch_bwd_t<T, 16, false, 4, SOFT>(g, p, s);                \
-        case 32: return launch_bwd_t<T, 32, false, 1, SOFT>(g, p, s);                \
-        case 64: return launch_bwd_t<T, 64, false, 1, SOFT>(g, p, s);                \
-      }                                                                              \
-    }                                                                                \
-    return hipErrorInvalidValue;                                                     \
+  hipError_t launch_variant_bwd<T, SOFT, RIGHT>(const Geometry& g, const BwdParams& p, \
+                                                hipStream_t s) {                     \
+    ACE_VARIANT_SWITCH(launch_bwd_t, T, SOFT, RIGHT)                                 \
   }
 
 }  // namespace ace

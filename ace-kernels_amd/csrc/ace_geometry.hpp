@@ -10,7 +10,8 @@ namespace ace {
 constexpr int kThreads = 256;           // threads per block (4 wave64)
 constexpr int kFrac = 30;               // fixed-point fraction bits of the sums
 constexpr int kMaxChannels = 64;        // largest C with a built kernel
-constexpr size_t kMaxHistLds = 64 * 1024;  // LDS budget of the histogram copies
+constexpr size_t kMaxHistLds = 32 * 1024;  // default LDS budget of the histogram copies
+constexpr int kMaxCopyCount = 2047;        // hard: voxels one copy may count (11-bit field)
 
 // Channel variants with a compiled kernel: the kernel keeps C logits of VEC
 // voxels in registers.  EXACT variants fix C at compile time; the others
@@ -27,7 +28,7 @@ inline Variant variant_for(int64_t C) {
   if (C == 3) return {3, true, 4};
   if (C == 4) return {4, true, 4};
   if (C <= 8) return {8, false, 4};
-  if (C == 16) return {16, true, 4};
+  if (C == 16) return {16, true, 2};
   if (C <= 16) return {16, false, 4};
   if (C <= 32) return {32, false, 1};
   return {64, false, 1};
@@ -37,11 +38,11 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Bytes of one histogram copy for a (C' * K)-bin block histogram.
-//   hard: u64 packed (count << 48 | sum p) + G (u32 count for labels,
-//         i64 fixed-point for per-channel targets)
+//   hard: u64 packed (count | label count | sum p), plus an i64 sum of the
+//         targets when they are per-channel values rather than labels
 //   soft: three i64 fixed-point sums W, P, G
 constexpr size_t hist_bytes_per_copy(int ck, bool soft, bool labels) {
-  return soft ? (size_t)ck * 24 : (size_t)ck * (labels ? 12 : 16);
+  return soft ? (size_t)ck * 24 : (size_t)ck * (labels ? 8 : 16);
 }
 
 struct Geometry {
@@ -67,7 +68,7 @@ struct Geometry {
 // keeping every block's tile a whole number of vector steps.
 inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
                               bool soft, bool include_background, bool labels,
-                              int steps_override = 0) {
+                              int steps_override = 0, int copies_override = 0) {
   Geometry g{};
   g.var = variant_for(C);
   g.C = (int)C;
@@ -77,14 +78,25 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   g.ck = g.CL * K;
   g.B = B;
   g.N = N;
+  // histogram copies: up to 32 (lane % 32), within the LDS budget
+  const size_t per_copy = hist_bytes_per_copy(g.ck, soft, labels);
+  int copies = copies_override > 0 ? copies_override : 32;
+  while (copies > 1 && per_copy * copies > (copies_override > 0 ? 160 * 1024 : kMaxHistLds))
+    copies /= 2;
+  g.copies = copies;
   const int64_t step_vox = (int64_t)kThreads * g.var.vec;
   int steps = steps_override;
   if (steps <= 0) {
     const int64_t total = B * (N > 0 ? N : 1);
-    const int64_t target_blocks = 2048;
+    const int64_t target_blocks = 1024;
     steps = (int)cdiv(total, step_vox * target_blocks);
     if (steps < 1) steps = 1;
     if (steps > 64) steps = 64;
+  }
+  if (!soft) {
+    // every copy counts at most kMaxCopyCount voxels of a tile
+    const int64_t max_steps = (int64_t)kMaxCopyCount * copies / step_vox;
+    if (steps > max_steps) steps = (int)(max_steps > 0 ? max_steps : 1);
   }
   g.steps = steps;
   g.tile_vox = step_vox * steps;
@@ -96,10 +108,6 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   if (gs > 64) gs = 64;
   g.gs = gs;
   g.gpb = cdiv(g.tiles, gs);
-  const size_t per_copy = hist_bytes_per_copy(g.ck, soft, labels);
-  int copies = 16;
-  while (copies > 1 && per_copy * copies > kMaxHistLds) copies /= 2;
-  g.copies = copies;
   const int n = soft ? 2 * K : K;
   g.tab_floats = align_up((size_t)(n + 2) + (soft ? (size_t)(2 * K + 2) : 0), 4);
   // the group-last block sums rows into 3 x CK u64 (LDS), and the last block

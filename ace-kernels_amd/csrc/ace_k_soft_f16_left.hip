@@ -1,0 +1,6 @@
+// Kernel instantiations: soft binning, __half logits, right=false.
+#include "ace_core.hpp"
+
+namespace ace {
+ACE_DEFINE_LAUNCHERS(__half, true, false)
+}  // namespace ace

@@ -206,6 +206,38 @@ def cpu_baseline(budget_s: float = 15.0):
     }
 
 
+def profile_kernels(workloads, launches: int) -> None:
+    """Launch only the hot-path kernels, for rocprofv3: per workload ``launches``
+    forwards and backwards (each its own kernel), then a plain copy kernel of
+    known size (256 MiB read + 256 MiB written) that calibrates FETCH_SIZE /
+    WRITE_SIZE."""
+    import torch
+
+    from ace_kernels.impls import hip_mi355x as hip
+    from ace_kernels.workloads import workload
+
+    for idx in workloads:
+        wl = workload(idx)
+        x, y = wl.make("cuda")
+        pl = hip.make_plan(x, y, wl.config)
+        _, coef, d, jac, _, _ = hip.hip_forward(pl, wl.config)
+        go = torch.ones((), device="cuda")
+        torch.cuda.synchronize()
+        for _ in range(launches):
+            hip.hip_forward(pl, wl.config)
+        for _ in range(launches):
+            hip.hip_backward(pl, coef, d, jac, go)
+        torch.cuda.synchronize()
+        log(f"profiled {wl.name}: {launches} x (ace forward, ace backward), "
+            f"fwd bytes {wl.input_bytes() + wl.target_bytes()}")
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(launches):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy kernel: {launches} x {src.numel() * 4} bytes read + written")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,6 +246,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--workloads", default="2,3", help="benchmark workloads (first = value)")
+    ap.add_argument("--profile-kernels", type=int, default=0, metavar="LAUNCHES",
+                    help="only launch the kernels LAUNCHES times each (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the loss on ONE GPU; --gpus above 1 is not supported "
@@ -227,6 +261,9 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     torch.cuda.set_device(0)
+    if args.profile_kernels:
+        profile_kernels([int(v) for v in args.workloads.split(",")], args.profile_kernels)
+        return 0
     flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
     results = []
     for idx in [int(v) for v in args.workloads.split(",")]:

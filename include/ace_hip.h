@@ -77,10 +77,11 @@ const char* ace_error_string(int code);
  */
 size_t ace_workspace_bytes(int64_t batch, int64_t channels, int64_t voxels,
                            int num_bins, int binning, int x_dtype,
-                           int include_background);
+                           int include_background, int target_kind);
 size_t ace_workspace_reset_bytes(int64_t batch, int64_t channels,
                                  int64_t voxels, int num_bins, int binning,
-                                 int x_dtype, int include_background);
+                                 int x_dtype, int include_background,
+                                 int target_kind);
 
 /*
  * Forward: per-bin statistics (W, P, G) of every (b, c') slice, then the

@@ -52,7 +52,7 @@ long long check_values(const float* table, int n, int right, const float* ps, lo
     if (std::isnan(p)) continue;
     int want = expected(table, n, p, right != 0);
     if (want > n - 1) want = n - 1;  // p above the last edge: kernels clamp
-    if (ace::bucket(p, (float)n, n, tab.data(), right != 0) != want) ++bad;
+    if ((right ? ace::bucket<true>(p, (float)n, n, tab.data()) : ace::bucket<false>(p, (float)n, n, tab.data())) != want) ++bad;
   }
   return bad;
 }
@@ -72,7 +72,7 @@ long long check_near_edges(const float* table, int n, int right, int ulps) {
       const float p = from_bits((uint32_t)u);
       int want = expected(table, n, p, right != 0);
       if (want > n - 1) want = n - 1;
-      if (ace::bucket(p, (float)n, n, tab.data(), right != 0) != want) ++bad;
+      if ((right ? ace::bucket<true>(p, (float)n, n, tab.data()) : ace::bucket<false>(p, (float)n, n, tab.data())) != want) ++bad;
     }
   }
   return bad;
@@ -88,7 +88,7 @@ long long check_range(const float* table, int n, int right, float lo, float hi) 
     const float p = from_bits((uint32_t)u);
     int want = expected(table, n, p, right != 0);
     if (want > n - 1) want = n - 1;
-    if (ace::bucket(p, (float)n, n, tab.data(), right != 0) != want) ++bad;
+    if ((right ? ace::bucket<true>(p, (float)n, n, tab.data()) : ace::bucket<false>(p, (float)n, n, tab.data())) != want) ++bad;
   }
   return bad;
 }
@@ -120,7 +120,7 @@ int check_clamped(const float* table, int n) {
                        -0.0f, 1.0000002f};
   for (float p : odd)
     for (int r = 0; r < 2; ++r) {
-      const int k = ace::bucket(p, (float)n, n, tab.data(), r != 0);
+      const int k = r ? ace::bucket<true>(p, (float)n, n, tab.data()) : ace::bucket<false>(p, (float)n, n, tab.data());
       if (k < 0 || k > n - 1) return 0;
     }
   return 1;

@@ -42,13 +42,13 @@ def test_error_strings() -> None:
 
 def test_workspace_sizes() -> None:
     lib = _lib.lib()
-    small = lib.ace_workspace_bytes(1, 4, 512, 20, _lib.HARD, _lib.F32, 1)
-    big = lib.ace_workspace_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F32, 1)
+    small = lib.ace_workspace_bytes(1, 4, 512, 20, _lib.HARD, _lib.F32, 1, 0)
+    big = lib.ace_workspace_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F32, 1, 0)
     assert 0 < small < big
     assert big < 64 << 20  # per-block partials only, not voxel-sized
-    reset = lib.ace_workspace_reset_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F32, 1)
+    reset = lib.ace_workspace_reset_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F32, 1, 0)
     assert 0 < reset < big and reset % 256 == 0
-    assert lib.ace_workspace_bytes(0, 4, 512, 20, 0, 0, 1) == 0
+    assert lib.ace_workspace_bytes(0, 4, 512, 20, 0, 0, 1, 0) == 0
 
 
 def test_invalid_arguments_rejected_before_launch() -> None:
