@@ -79,13 +79,6 @@ int env_copies() {
   return (c == 1 || c == 2 || c == 4 || c == 8 || c == 16 || c == 32 || c == 64) ? c : 0;
 }
 
-// Cross-block reduction: "tree" (group tickets, default) or "direct"
-// (every block adds its partial to the final sums with integer atomics).
-int env_reduce_mode() {
-  const char* v = getenv("ACE_FWD_REDUCE");
-  return (v && v[0] == 'd') ? kReduceDirect : kReduceTree;
-}
-
 size_t elem_size(int dtype) { return dtype == ACE_F32 ? 4 : 2; }
 
 bool aligned_to(const void* p, size_t a) {
@@ -157,7 +150,7 @@ size_t ace_workspace_reset_bytes(int64_t batch, int64_t channels, int64_t voxels
                                    include_background != 0,
                                    target_kind == ACE_TARGET_LABELS_I64,
                                    env_steps("ACE_FWD_STEPS"), env_copies());
-  return g.ws_counters;
+  return g.ws_bytes;
 }
 
 int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
@@ -213,9 +206,8 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   p.ctr = reinterpret_cast<int*>(ws);
   p.fin = reinterpret_cast<unsigned long long*>(ws + g.off_fin);
-  p.part = reinterpret_cast<long long*>(ws + g.off_part);
-  p.mode = env_reduce_mode();
-  p.epi_batch = g.epi_batch;
+  p.reps = g.reps;
+  p.lchunk = g.lchunk;
   p.coef = coef;
   p.d = diff;
   p.jac = jac;

@@ -10,10 +10,10 @@
 // bitwise deterministic with no float atomics.  Lane l of a wave adds into
 // copy (l % copies) of the histogram, copies laid out bin-major, so the lanes
 // one LDS cycle serves hit distinct banks whatever their bins.  Each block
-// then publishes an integer partial; the last block of each group (ticket
-// counter) sums its group into the final sums with integer atomics, and the
-// last group's block runs the epilogue (d, coef, per-class error, jac, loss)
-// and leaves counters and sums zero for the next call.
+// then adds its sums into one of a few replicas of its batch index's final
+// sums with integer atomics; ticket counters select the block that runs the
+// epilogue of each batch index (d, coef, per-class error, jac) and the one
+// that sums the loss.  Every call leaves counters and sums zero for the next.
 //
 // Backward (one launch): recompute the activation and the bins from the
 // logits with the same device functions (identical bits), gather coef (and d
@@ -38,7 +38,6 @@ namespace ace {
 enum { kActNone = 0, kActSoftmax = 1, kActSigmoid = 2 };
 enum { kRedMean = 0, kRedSum = 1, kRedNone = 2 };
 enum { kTgtLabels = 0, kTgtOnehot = 1 };
-enum { kReduceTree = 0, kReduceDirect = 1 };
 
 // Packed hard-binning histogram word: count | label count | sum p.
 //   bits [53, 64): voxels in the bin (<= 2047 per copy and block)
@@ -56,15 +55,15 @@ struct FwdParams {
   int64_t gs;
   int64_t gpb;
   int B, C, off, K, act, tk, copies, vec_ok, ignore_empty, red;
-  int mode;            // kReduceTree or kReduceDirect
-  int epi_batch;       // batch indices per epilogue pass
+  int reps;            // replicas of each batch index's final sums
+  int lchunk;          // log2 of the copies one lane adds before unpacking
   float empty_w;
   const float* btab;   // bucket table (K or 2K upper boundaries)
   const float* rtab;   // soft centre table (2K + 2)
   const float* clsw;   // C' class weights or null
-  long long* part;     // [nblk][3][CK] block partials (tree mode)
-  unsigned long long* fin;  // [B][3][CK] zeroed final sums (reset by the epilogue)
-  int* ctr;            // [B * gpb + 1] zeroed ticket counters
+  unsigned long long* fin;  // [B][reps][3][CK] zeroed final sums (reset by the epilogues)
+  int* ctr;            // zeroed ticket counters, kCtrStride ints apart:
+                       // [B * gpb] groups, [B] batch indices, [1] loss
   float* coef;
   float* d;
   float* jac;
@@ -192,9 +191,28 @@ __device__ __forceinline__ float div_rn(float a, float b, float y) {
 
 // ------------------------------------------------------------ activation
 
+// exp(x) for the softmax arguments x = logit - max <= 0: 2^(x log2 e) with the
+// usual split of x log2 e into ph + pl (log2 e rounded to float, the product's
+// rounding error by fma, plus x times the remainder of log2 e), the integer
+// part of ph taken out by rint/ldexp so that v_exp_f32 sees a reduced argument
+// that carries pl.  This is the range reduction ROCm's expf uses; its
+// overflow/underflow selects are replaced by one clamp of x at -104, below
+// which every result underflows (x <= 0 cannot overflow).  Measured on MI355X
+// against a float64 exp for every float x in [-104, 0]: max error 0.857 ulp,
+// no result off by more than 1 ulp -- the same figures as ROCm's expf.
+__device__ __forceinline__ float exp_neg(float x) {
+  x = fmaxf(x, -104.0f);
+  const float ph = x * 0x1.715476p+0f;
+  float pl = fmaf(x, 0x1.715476p+0f, -ph);
+  pl = fmaf(x, 0x1.4ae0bep-26f, pl);
+  const float e = rintf(ph);
+  const float a = (ph - e) + pl;
+  return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(a), (int)e);
+}
+
 // In place: logits -> probabilities.  Softmax follows torch.softmax: max over
 // channels, e_c = exp(x_c - max), s = sequential sum over c, p_c = e_c / s
-// (IEEE quotient), with ROCm's accurate expf.  Sigmoid: 1 / (1 + exp(-x)).
+// (IEEE quotient), with exp_neg.  Sigmoid: 1 / (1 + exp(-x)).
 template <int CMAX, bool EXACT>
 __device__ __forceinline__ void activate(float (&x)[CMAX], int nc, int act) {
   if (act == kActSoftmax) {
@@ -206,7 +224,7 @@ __device__ __forceinline__ void activate(float (&x)[CMAX], int nc, int act) {
 #pragma unroll
     for (int c = 0; c < CMAX; ++c)
       if (EXACT || c < nc) {
-        x[c] = expf(x[c] - m);
+        x[c] = exp_neg(x[c] - m);
         s += x[c];
       }
     const float y = rcp_rn(s);
@@ -270,12 +288,31 @@ __device__ __forceinline__ void lds_add(long long* p, long long v) {
 // increments a ticket, and the block that draws the last ticket reads the data
 // with sc1 loads.  No dirty L2 line holds shared data, so no write-back is
 // needed, and no stale line can be read.
+//
+// Device-scope atomics are serialised per cache line at the memory side
+// (about 10-17 ns per wave request on MI355X, measured): 1024 blocks
+// incrementing one counter take ~11 us, and counters sharing a line contend
+// as if they were one.  So every ticket counter has its own 256-byte line and
+// takes at most a few dozen arrivals (groups of <= 16 blocks, then the groups
+// of a batch index).  The final sums take one request per block and line;
+// blocks finish spread over several microseconds, and up to kMaxReps replicas
+// (one per kRepTiles blocks) trade that contention against the epilogue's
+// loads -- 2 replicas for 512 blocks per batch index measured fastest.
 __device__ __forceinline__ void store_dev(long long* p, long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned long long load_dev(const unsigned long long* p) {
   return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait until this thread's global stores and atomics have completed.
 __device__ __forceinline__ void wait_own_writes() {
@@ -300,6 +337,36 @@ __device__ __forceinline__ void load_tables(float* lds, const float* btab, const
   }
   for (int i = threadIdx.x; i < nrepl; i += kThreads) lds[n + 2 + i] = rtab[i];
 }
+
+// A thread's share of the LDS tables -- entries tid and tid + kThreads of the
+// padded bucket table and of the centre table -- held in registers, so that a
+// kernel can issue these loads, then its first tile's loads, and only then
+// wait for the tables (in-order vmcnt) and write them to LDS.
+struct TableRegs {
+  float b[2], r[2];
+  __device__ __forceinline__ void load(const float* btab, const float* rtab, int n, int nrepl) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = (int)threadIdx.x + u * kThreads;
+      b[u] = i == 0 ? -__builtin_inff() : (i <= n ? btab[i - 1] : __builtin_inff());
+      r[u] = i < nrepl ? rtab[i] : 0.0f;
+    }
+  }
+  __device__ __forceinline__ void store(float* lds, const float* btab, const float* rtab, int n,
+                                        int nrepl) const {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = (int)threadIdx.x + u * kThreads;
+      if (i < n + 2) lds[i] = b[u];
+      if (i < nrepl) lds[n + 2 + i] = r[u];
+    }
+    // tables longer than 2 x kThreads entries
+    for (int i = (int)threadIdx.x + 2 * kThreads; i < n + 2; i += kThreads)
+      lds[i] = i == n + 1 ? __builtin_inff() : btab[i - 1];
+    for (int i = (int)threadIdx.x + 2 * kThreads; i < nrepl; i += kThreads)
+      lds[n + 2 + i] = rtab[i];
+  }
+};
 
 // ------------------------------------------------------------ tiles
 
@@ -404,185 +471,237 @@ __device__ __forceinline__ void fwd_accumulate(const FwdParams& P, const Hist& H
   }
 }
 
-// ---- end of a forward block: publish the block's sums, and in the last
-// block of a group / of the grid run the reductions and the epilogue
+// Sum of v over the 64 lanes of a wave, in the same butterfly order in every
+// lane (bit-identical result everywhere; float addition is commutative).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Ticket counter i of the workspace (counters are kCtrStride ints apart).
+__device__ __forceinline__ int* counter(const FwdParams& P, int64_t i) {
+  return P.ctr + i * kCtrStride;
+}
+
+// Epilogue of batch index b (kernels/epilogue.py:23-82): final sums -> d, W,
+// G per bin; per class row: K_ne, f, coef, jac.  Runs in the block that drew
+// the last ticket of batch b; it also leaves b's final sums zero.
 template <bool SOFT>
-__device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, unsigned char* hist,
-                                           int CK, int CL, int b, int64_t tile, int64_t blk,
-                                           bool labels) {
+__device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char* hist, int CK,
+                                               int CL, int b) {
   const int tid = threadIdx.x;
   const int K = P.K;
-  const int R = P.copies;
-  // ---- block partial: sum the copies -> W3 = 3 x CK fixed-point values
   const int W3 = 3 * CK;
-  const bool direct = P.mode == kReduceDirect;
-  unsigned long long* fin_b = P.fin + (int64_t)b * W3;
-  long long* part = P.part + blk * (int64_t)W3;
-  for (int t = tid; t < CK; t += kThreads) {
-    long long s0 = 0, s1 = 0, s2 = 0;
-    for (int r = 0; r < R; ++r) {
-      // skew the copy index by t: neighbouring threads read neighbouring banks
-      const int slot = t * R + ((r + t) & (R - 1));
-      if constexpr (!SOFT) {
-        const unsigned long long a = H.a[slot];
-        const unsigned long long hi = (a + (1ull << (kShiftG - 1))) >> kShiftG;
-        s0 += (long long)((hi >> (kShiftN - kShiftG)) << kFrac);
-        s1 += (long long)(a - (hi << kShiftG));
-        s2 += labels ? (long long)((hi & ((1ull << (kShiftN - kShiftG)) - 1)) << kFrac)
-                     : H.g1[slot];
-      } else {
-        s0 += H.w[slot];
-        s1 += H.p[slot];
-        s2 += H.g[slot];
-      }
-    }
-    if (direct) {
-      // integer atomics into the final sums: order-independent, deterministic
-      if (s0) atomicAdd(&fin_b[t], (unsigned long long)s0);
-      if (s1) atomicAdd(&fin_b[CK + t], (unsigned long long)s1);
-      if (s2) atomicAdd(&fin_b[2 * CK + t], (unsigned long long)s2);
-    } else {
-      store_dev(&part[t], s0);
-      store_dev(&part[CK + t], s1);
-      store_dev(&part[2 * CK + t], s2);
-    }
-  }
-
-  __shared__ int s_last;
-  wait_own_writes();
-  __syncthreads();
-  const int64_t ngroups = (int64_t)P.B * P.gpb;  // index of the top counter
-  int64_t arrivals = P.B * P.tiles;              // direct: every block reports
-  if (!direct) {
-    // ---- group ticket: the last block of the group sums the group's rows
-    const int64_t g = tile / P.gs;
-    const int64_t gidx = (int64_t)b * P.gpb + g;
-    const int64_t gsize = min(P.gs, P.tiles - g * P.gs);
-    if (tid == 0) {
-      const int prev = ticket(&P.ctr[gidx]);
-      s_last = (prev == (int)gsize - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    unsigned long long* acc = reinterpret_cast<unsigned long long*>(hist);
-    for (int t = tid; t < W3; t += kThreads) acc[t] = 0ull;
-    __syncthreads();
-    // the group's partials are gsize contiguous rows of W3 values: read them
-    // with every thread, four independent loads in flight per thread
-    const unsigned long long* src = reinterpret_cast<const unsigned long long*>(
-        P.part + ((int64_t)b * P.tiles + g * P.gs) * W3);
-    const int total = (int)gsize * W3;
-    for (int i0 = tid; i0 < total; i0 += 4 * kThreads) {
-      unsigned long long v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * kThreads;
-        v[u] = i < total ? load_dev(src + i) : 0ull;
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (v[u]) lds_add(&acc[(i0 + u * kThreads) % W3], v[u]);
-    }
-    __syncthreads();
-    for (int t = tid; t < W3; t += kThreads)
-      if (acc[t]) atomicAdd(&fin_b[t], acc[t]);
-    if (tid == 0) __hip_atomic_store(&P.ctr[gidx], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    wait_own_writes();
-    __syncthreads();
-    arrivals = ngroups;
-  }
-  // ---- top ticket: the last arrival runs the epilogue
-  if (tid == 0) {
-    const int prev = ticket(&P.ctr[ngroups]);
-    s_last = (prev == (int)arrivals - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-
-  // ---- epilogue (one block), `bc` batch indices at a time:
-  // sums -> d, W, G per bin (LDS); per (b, c') row: K_ne, f, coef, jac
-  const int bc = P.epi_batch;
+  const int reps = P.reps;
   float* sd = reinterpret_cast<float*>(hist);
-  float* sw = sd + (size_t)bc * CK;
-  float* sg = sw + (size_t)bc * CK;
-  float* sf = sg + (size_t)bc * CK;
-  unsigned char* se = reinterpret_cast<unsigned char*>(sf + (size_t)bc * CK);
+  float* sw = sd + CK;
+  float* sg = sw + CK;
+  unsigned char* se = reinterpret_cast<unsigned char*>(sg + CK);
+  unsigned long long* fb = P.fin + (int64_t)b * reps * W3;
   const int64_t BCK = (int64_t)P.B * CK;
   const double dscale = 1.0 / 1073741824.0;
-  const int rows = P.B * CL;
-  float total = 0.0f;  // thread 0: sequential sum of the per-class errors
-  for (int b0 = 0; b0 < P.B; b0 += bc) {
-    const int nb = min(bc, P.B - b0);
-    for (int i = tid; i < nb * CK; i += kThreads) {
-      const int bb = b0 + i / CK;
-      const int t = i - (i / CK) * CK;
-      unsigned long long* fb = P.fin + (int64_t)bb * W3;
-      const long long s0 = (long long)load_dev(&fb[t]);
-      const long long s1 = (long long)load_dev(&fb[CK + t]);
-      const long long s2 = (long long)load_dev(&fb[2 * CK + t]);
-      // leave the accumulator zero for the next call
-      __hip_atomic_store(&fb[t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&fb[CK + t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&fb[2 * CK + t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const double Wd = (double)s0 * dscale;
-      const double Pd = (double)s1 * dscale;
-      const double Gd = (double)s2 * dscale;
-      if (P.stats) {
-        P.stats[(int64_t)bb * CK + t] = Wd;
-        P.stats[BCK + (int64_t)bb * CK + t] = Pd;
-        P.stats[2 * BCK + (int64_t)bb * CK + t] = Gd;
+  for (int t = tid; t < CK; t += kThreads) {
+    // every replica's three sums in flight at once (reps <= kMaxReps)
+    long long s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int r = 0; r < kMaxReps; ++r) {
+      if (r < reps) {
+        unsigned long long* f = fb + (int64_t)r * W3;
+        s0 += (long long)load_dev(&f[t]);
+        s1 += (long long)load_dev(&f[CK + t]);
+        s2 += (long long)load_dev(&f[2 * CK + t]);
       }
-      const float Wf = (float)Wd;
-      const float Pf = (float)Pd;
-      const float Gf = (float)Gd;
-      const bool empty = SOFT ? !(Wf >= P.empty_w) : (Wf == 0.0f);
-      const float dd = empty ? 0.0f : (Pf / Wf - Gf / Wf);
-      sd[i] = dd;
-      sw[i] = Wf;
-      sg[i] = Gf;
-      se[i] = empty ? 1 : 0;
-      P.d[(int64_t)bb * CK + t] = dd;
     }
-    __syncthreads();
-    for (int r = tid; r < nb * CL; r += kThreads) {
-      const int bb = b0 + r / CL;
-      const int cl = r - (r / CL) * CL;
-      const int base = (r / CL) * CK + cl * K;
-      int kne = 0;
-      float err = 0.0f, gsum = 0.0f;
-      for (int k = 0; k < K; ++k) {
-        if (!se[base + k]) {
-          ++kne;
-          err += fabsf(sd[base + k]);
-        }
-        gsum += sg[base + k];
+    for (int r = 0; r < reps; ++r) {
+      unsigned long long* f = fb + (int64_t)r * W3;
+      store_dev(&f[t], 0ull);
+      store_dev(&f[CK + t], 0ull);
+      store_dev(&f[2 * CK + t], 0ull);
+    }
+    const double Wd = (double)s0 * dscale;
+    const double Pd = (double)s1 * dscale;
+    const double Gd = (double)s2 * dscale;
+    const int64_t o = (int64_t)b * CK + t;
+    if (P.stats) {
+      P.stats[o] = Wd;
+      P.stats[BCK + o] = Pd;
+      P.stats[2 * BCK + o] = Gd;
+    }
+    const float Wf = (float)Wd;
+    const float Pf = (float)Pd;
+    const float Gf = (float)Gd;
+    const bool empty = SOFT ? !(Wf >= P.empty_w) : (Wf == 0.0f);
+    const float dd = empty ? 0.0f : (Pf / Wf - Gf / Wf);
+    sd[t] = dd;
+    sw[t] = Wf;
+    sg[t] = Gf;
+    se[t] = empty ? 1 : 0;
+    P.d[o] = dd;
+  }
+  __syncthreads();
+  // one wave per class row
+  const int lane = tid & 63;
+  const int rows = P.B * CL;
+  for (int cl = tid >> 6; cl < CL; cl += kThreads / 64) {
+    const int base = cl * K;
+    int kne = 0;
+    float err = 0.0f, gsum = 0.0f;
+    for (int k = lane; k < K; k += 64) {
+      if (!se[base + k]) {
+        ++kne;
+        err += fabsf(sd[base + k]);
       }
-      const float fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
-      const float present = gsum > 0.0f ? 1.0f : 0.0f;
-      const float kf = (float)(kne > 0 ? kne : 1);
-      for (int k = 0; k < K; ++k) {
-        const float dd = sd[base + k];
-        const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
-        P.coef[(int64_t)bb * CK + cl * K + k] = se[base + k] ? 0.0f : sgn / (kf * sw[base + k]);
-      }
+      gsum += sg[base + k];
+    }
+    kne = wave_sum(kne);
+    err = wave_sum(err);
+    gsum = wave_sum(gsum);
+    const float fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
+    const float present = gsum > 0.0f ? 1.0f : 0.0f;
+    const float kf = (float)(kne > 0 ? kne : 1);
+    for (int k = lane; k < K; k += 64) {
+      const float dd = sd[base + k];
+      const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
+      P.coef[(int64_t)b * CK + base + k] = se[base + k] ? 0.0f : sgn / (kf * sw[base + k]);
+    }
+    if (lane == 0) {
       const float w = P.clsw ? P.clsw[cl] : 1.0f;
       float fw = P.ignore_empty ? fcls * present : fcls;
       fw = fw * w;
       float jac = P.ignore_empty ? present * w : w;
       if (P.red == kRedMean) jac = jac / (float)rows;
-      P.f[bb * CL + cl] = fw;
-      P.jac[bb * CL + cl] = jac;
-      sf[r] = fw;
+      store_dev(&P.f[b * CL + cl], fw);
+      P.jac[b * CL + cl] = jac;
     }
-    __syncthreads();
-    if (tid == 0)
-      for (int r = 0; r < nb * CL; ++r) total += sf[r];
-    __syncthreads();
   }
+}
+
+// Sums the R histogram copies of every bin and adds the block's 3 x CK sums
+// into `fin` with integer atomics.  Q = R / chunk neighbouring lanes share a
+// bin: each adds `chunk` copies (hard: packed words, added before decoding --
+// the geometry keeps chunk x per-copy counts within the 11-bit fields), then
+// the Q lanes combine with shuffles and the first one issues the atomics, so
+// one wave request covers 64 / Q consecutive bins.  The copy index is skewed
+// by the bin so that the lanes of a wave read distinct bank pairs.
+template <bool SOFT>
+__device__ __forceinline__ void block_sums(const FwdParams& P, const Hist& H, int CK, bool labels,
+                                           unsigned long long* fin) {
+  const int tid = threadIdx.x;
+  const int R = P.copies;
+  const int chunk = 1 << P.lchunk;
+  const int lq = __builtin_ctz((unsigned)R) - P.lchunk;
+  const int Q = 1 << lq;
+  const int total = CK << lq;
+  for (int base = 0; base < total; base += kThreads) {
+    const int i = base + tid;
+    const int t = i >> lq;
+    const int part = i & (Q - 1);
+    long long s0 = 0, s1 = 0, s2 = 0;
+    if (t < CK) {
+      const int w0 = t * R + part * chunk;
+      if constexpr (!SOFT) {
+        unsigned long long a = 0;
+        long long gy = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (j < chunk) {
+            const int w = w0 + ((j + t) & (chunk - 1));
+            a += H.a[w];
+            if (!labels) gy += H.g1[w];
+          }
+        }
+        // the sum-p field is signed (probabilities outside [0, 1] without an
+        // activation): round the upper fields so that it decodes in
+        // [-2^41, 2^41)
+        const unsigned long long hi = (a + (1ull << (kShiftG - 1))) >> kShiftG;
+        s0 = (long long)((hi >> (kShiftN - kShiftG)) << kFrac);
+        s1 = (long long)(a - (hi << kShiftG));
+        s2 = labels ? (long long)((hi & ((1ull << (kShiftN - kShiftG)) - 1)) << kFrac) : gy;
+      } else {
+        for (int j = 0; j < chunk; ++j) {
+          const int w = w0 + ((j + t) & (chunk - 1));
+          s0 += H.w[w];
+          s1 += H.p[w];
+          s2 += H.g[w];
+        }
+      }
+    }
+    for (int o = 1; o < Q; o <<= 1) {
+      s0 += __shfl_xor(s0, o, 64);
+      s1 += __shfl_xor(s1, o, 64);
+      s2 += __shfl_xor(s2, o, 64);
+    }
+    if (t < CK && part == 0) {
+      if (s0) atomicAdd(&fin[t], (unsigned long long)s0);
+      if (s1) atomicAdd(&fin[CK + t], (unsigned long long)s1);
+      if (s2) atomicAdd(&fin[2 * CK + t], (unsigned long long)s2);
+    }
+  }
+}
+
+// ---- end of a forward block.  Adds the block's sums into replica
+// (tile % reps) of batch b's final sums (fixed point: exact and
+// order-independent).  Ticket counters, each on its own 256-byte line, then
+// pick the last block of each group of gs tiles, the last group of batch b
+// (which runs b's epilogue) and the last batch (which sums the per-class
+// errors into the loss in a fixed order).
+template <bool SOFT>
+__device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, unsigned char* hist,
+                                           int CK, int CL, int b, int64_t tile, bool labels) {
+  const int tid = threadIdx.x;
+  const int W3 = 3 * CK;
+  block_sums<SOFT>(P, H, CK, labels, P.fin + ((int64_t)b * P.reps + tile % P.reps) * W3);
+  __shared__ int s_last;
+  wait_own_writes();
+  __syncthreads();
   if (tid == 0) {
+    const int64_t g = tile / P.gs;
+    const int64_t gsize = min(P.gs, P.tiles - g * P.gs);
+    int last = 0;
+    int* gc = counter(P, (int64_t)b * P.gpb + g);
+    if (ticket(gc) == (int)gsize - 1) {
+      __hip_atomic_store(gc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int* bc = counter(P, (int64_t)P.B * P.gpb + b);
+      last = ticket(bc) == (int)P.gpb - 1;
+      if (last) __hip_atomic_store(bc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  batch_epilogue<SOFT>(P, hist, CK, CL, b);
+  if (P.red == kRedNone) return;
+
+  // ---- loss: the last batch epilogue sums the B x C' per-class errors
+  wait_own_writes();
+  __syncthreads();
+  if (tid == 0) {
+    int* tc = counter(P, (int64_t)P.B * P.gpb + P.B);
+    const int last = ticket(tc) == P.B - 1;
+    if (last) __hip_atomic_store(tc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int rows = P.B * CL;
+  float part = 0.0f;
+  for (int i = tid; i < rows; i += kThreads) part += load_dev(&P.f[i]);
+  part = wave_sum(part);
+  float* sp = reinterpret_cast<float*>(hist);
+  if ((tid & 63) == 0) sp[tid >> 6] = part;
+  __syncthreads();
+  if (tid == 0) {
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) total += sp[w];
     if (P.red == kRedMean) total = total / (float)rows;
-    if (P.red != kRedNone) P.loss[0] = total;
-    __hip_atomic_store(&P.ctr[ngroups], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    P.loss[0] = total;
   }
 }
 
@@ -664,7 +783,7 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
     fwd_accumulate<CMAX, EXACT, 1, SOFT, RIGHT>(P, H, btab, repl, nc, copy, xv, lab, yv, labels);
   }
   __syncthreads();
-  fwd_finish<SOFT>(P, H, hist, CK, CL, b, tile, blk, labels);
+  fwd_finish<SOFT>(P, H, hist, CK, CL, b, tile, labels);
 }
 
 // ------------------------------------------------------------ backward
@@ -836,6 +955,12 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
 // in [0, 1], so the bin index needs no float clamp and the fixed-point terms
 // are non-negative.
 
+// Word of bin k in a histogram copy whose bins are 1 << lsh bytes apart.
+__device__ __forceinline__ unsigned long long* bin_at(unsigned long long* base, int k, int lsh) {
+  return reinterpret_cast<unsigned long long*>(reinterpret_cast<unsigned char*>(base) +
+                                               ((uint32_t)k << lsh));
+}
+
 template <int C, int VEC>
 struct FastTile {
   float x[C][VEC];
@@ -870,15 +995,42 @@ __device__ __forceinline__ uint32_t fast_label(long long v) {
   return (hi == 0u && lo < (uint32_t)C) ? lo : 0xffffffffu;
 }
 
+// max of raw logits with v_max3_f32 / v_max_f32 directly: fmaxf would first
+// canonicalise each loaded value (one more instruction per operand)
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float vmax2(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+template <int C>
+__device__ __forceinline__ float max_of(const float (&x)[C]) {
+  if constexpr (C == 1) {
+    return x[0];
+  } else if constexpr (C == 2) {
+    return vmax2(x[0], x[1]);
+  } else {
+    float m = vmax3(x[0], x[1], x[2]);
+    int c = 3;
+#pragma unroll
+    for (; c + 1 < C; c += 2) m = vmax3(m, x[c], x[c + 1]);
+    if (c < C) m = vmax2(m, x[c]);
+    return m;
+  }
+}
+
 template <int C>
 __device__ __forceinline__ void softmax_fast(float (&x)[C]) {
-  float m = x[0];
+  const float m = max_of<C>(x);
+  x[0] = exp_neg(x[0] - m);
+  float s = x[0];  // == 0 + x[0]: the sum starts from +0
 #pragma unroll
-  for (int c = 1; c < C; ++c) m = fmaxf(m, x[c]);
-  float s = 0.0f;
-#pragma unroll
-  for (int c = 0; c < C; ++c) {
-    x[c] = expf(x[c] - m);
+  for (int c = 1; c < C; ++c) {
+    x[c] = exp_neg(x[c] - m);
     s += x[c];
   }
   const float y = rcp_rn(s);
@@ -887,10 +1039,11 @@ __device__ __forceinline__ void softmax_fast(float (&x)[C]) {
 }
 
 // One tile into the histogram copies.  hb[c]: this lane's copy of channel c's
-// bin 0 (u64 words), bins `R` words apart (R = 1 << lr).
+// bin 0 (u64 words), bins R words = 1 << lsh bytes apart.  skip0: channel 0
+// (background) is not in the loss.
 template <int C, int VEC, bool SOFT, bool RIGHT>
 __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const float* tab,
-                                                const float* repl, int K, int off, int lr,
+                                                const float* repl, int K, bool skip0, int lsh,
                                                 unsigned long long* const (&hb)[C],
                                                 const size_t words) {
   const float nf = (float)(SOFT ? 2 * K : K);
@@ -904,12 +1057,12 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
     if constexpr (!SOFT) {
 #pragma unroll
       for (int c = 0; c < C; ++c) {
-        if (c < off) continue;
+        if (c == 0 && skip0) continue;
         const int k = bucket<RIGHT, false>(p[c], nf, K, tab);
         const uint32_t q = (uint32_t)rintf(p[c] * 1073741824.0f);
         const uint32_t hi = (lab == (uint32_t)c) ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
                                                  : (1u << (kShiftN - 32));
-        lds_add(hb[c] + ((size_t)k << lr), ((unsigned long long)hi << 32) | q);
+        lds_add(bin_at(hb[c], k, lsh), ((unsigned long long)hi << 32) | q);
       }
     } else {
       unsigned long long* gl = hb[0];
@@ -917,10 +1070,10 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
       uint32_t glw = 0u, grw = 0u;
 #pragma unroll
       for (int c = 0; c < C; ++c) {
-        if (c < off) continue;
+        if (c == 0 && skip0) continue;
         const SoftW w = soft_assign<RIGHT, false>(p[c], K, nf, tab, repl);
-        unsigned long long* sl = hb[c] + ((size_t)w.l << lr);
-        unsigned long long* sr = hb[c] + ((size_t)w.r << lr);
+        unsigned long long* sl = bin_at(hb[c], w.l, lsh);
+        unsigned long long* sr = bin_at(hb[c], w.r, lsh);
         const uint32_t ql = (uint32_t)rintf(w.lw * 1073741824.0f);
         const uint32_t qr = (uint32_t)rintf(w.rw * 1073741824.0f);
         lds_add(sl, (unsigned long long)ql);
@@ -933,7 +1086,7 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
         glw = hit ? ql : glw;
         grw = hit ? qr : grw;
       }
-      if (lab != 0xffffffffu && lab >= (uint32_t)off) {
+      if (lab != 0xffffffffu && !(lab == 0u && skip0)) {
         lds_add(gl + 2 * words, (unsigned long long)glw);
         lds_add(gr + 2 * words, (unsigned long long)grw);
       }
@@ -952,6 +1105,8 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   const int CK = CL * K;
   const int R = P.copies;
   const int lr = __builtin_ctz((unsigned)R);
+  const int lsh = lr + 3;
+  const bool skip0 = off != 0;
   const int tid = threadIdx.x;
   const int64_t blk = blockIdx.x;
   const int b = (int)(blk / P.tiles);
@@ -966,19 +1121,7 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   H.p = H.w + (size_t)CK * R;
   H.g = H.p + (size_t)CK * R;
   const size_t hist_words = (hist_bytes_per_copy(CK, SOFT, true) * (size_t)R + 7) / 8;
-  load_tables(tabs, P.btab, P.rtab, n, SOFT ? 2 * K + 2 : 0);
-  {
-    unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
-    for (size_t i = tid; i < hist_words; i += kThreads) h64[i] = 0ull;
-  }
-  __syncthreads();
-  const float* tab = tabs;
-  const float* repl = tabs + n + 2;
-  const int copy = tid & (R - 1);
-  unsigned long long* hb[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c)
-    hb[c] = H.a + ((size_t)((c < off ? 0 : c - off) * K) << lr) + copy;
+  const int nrepl = SOFT ? 2 * K + 2 : 0;
 
   const int64_t N = P.N;
   const int64_t t0 = tile * P.tile_vox;
@@ -993,33 +1136,51 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   const int stride = kThreads * VEC;
   const int nsteps = nfull / stride;  // steps in which every thread has a full vector
 
+  // table loads, then the first tile's loads; the tables are written to LDS
+  // and the histogram cleared while the tile is in flight
+  TableRegs treg;
+  treg.load(P.btab, P.rtab, n, nrepl);
+  FastTile<C, VEC> ta, tb;
+  const uint32_t v0 = (uint32_t)(tid * VEC);
+  if (nsteps > 0) fast_load<T, C, VEC>(ta, xr, lr_, v0, true);
+  treg.store(tabs, P.btab, P.rtab, n, nrepl);
+  {
+    unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
+    for (size_t i = tid; i < hist_words; i += kThreads) h64[i] = 0ull;
+  }
+  __syncthreads();
+  const float* tab = tabs;
+  const float* repl = tabs + n + 2;
+  const int copy = tid & (R - 1);
+  unsigned long long* hb[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    hb[c] = H.a + ((size_t)((c < off ? 0 : c - off) * K) << lr) + copy;
+
   if (nsteps > 0) {
-    FastTile<C, VEC> ta, tb;
-    const uint32_t v0 = (uint32_t)(tid * VEC);
-    fast_load<T, C, VEC>(ta, xr, lr_, v0, true);
     for (int i = 0; i < nsteps; i += 2) {
       const uint32_t va = v0 + (uint32_t)(i * stride);
       const uint32_t vb = (i + 1 < nsteps) ? va + (uint32_t)stride : va;
       fast_load<T, C, VEC>(tb, xr, lr_, vb, true);
-      fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, off, lr, hb, words);
+      fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, skip0, lsh, hb, words);
       const uint32_t vc = (i + 2 < nsteps) ? va + 2u * (uint32_t)stride : vb;
       fast_load<T, C, VEC>(ta, xr, lr_, vc, true);
-      if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, off, lr, hb, words);
+      if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, skip0, lsh, hb, words);
     }
   }
   // remaining full vectors (not every thread has one), then single voxels
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
     fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, true);
-    fast_accumulate<C, VEC, SOFT, RIGHT>(t, tab, repl, K, off, lr, hb, words);
+    fast_accumulate<C, VEC, SOFT, RIGHT>(t, tab, repl, K, skip0, lsh, hb, words);
   }
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     FastTile<C, 1> t;
     fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, true);
-    fast_accumulate<C, 1, SOFT, RIGHT>(t, tab, repl, K, off, lr, hb, words);
+    fast_accumulate<C, 1, SOFT, RIGHT>(t, tab, repl, K, skip0, lsh, hb, words);
   }
   __syncthreads();
-  fwd_finish<SOFT>(P, H, hist, CK, CL, b, tile, blk, true);
+  fwd_finish<SOFT>(P, H, hist, CK, CL, b, tile, true);
 }
 
 // Backward of one tile, in place in t.x (logits in, gradient out).
@@ -1041,7 +1202,7 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       gp[c] = 0.0f;
-      if (c < off) continue;
+      if (c == 0 && off != 0) continue;
       const int cl = c - off;
       if constexpr (!SOFT) {
         const int k = bucket<RIGHT, false>(p[c], nf, K, tab);
@@ -1081,18 +1242,7 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   float* scoef = tabs + tab_floats;
   float* sdd = scoef + CK;
   float* sg = sdd + (SOFT ? CK : 0);
-  load_tables(tabs, P.btab, P.rtab, n, SOFT ? 2 * K + 2 : 0);
-  for (int i = tid; i < CK; i += kThreads) {
-    scoef[i] = P.coef[(int64_t)b * CK + i];
-    if (SOFT) sdd[i] = P.d[(int64_t)b * CK + i];
-  }
-  for (int i = tid; i < CL; i += kThreads) {
-    const float go = P.go_per_class ? P.go[b * CL + i] : P.go[0];
-    sg[i] = P.jac[b * CL + i] * go;
-  }
-  __syncthreads();
-  const float* tab = tabs;
-  const float* repl = tabs + n + 2;
+  const int nrepl = SOFT ? 2 * K + 2 : 0;
 
   const int64_t N = P.N;
   const int64_t t0 = tile * P.tile_vox;
@@ -1109,10 +1259,36 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   const int stride = kThreads * VEC;
   const int nsteps = nfull / stride;
 
+  // tables and this thread's first coefficients, then the first tile's loads;
+  // LDS is filled while the tile is in flight
+  TableRegs treg;
+  treg.load(P.btab, P.rtab, n, nrepl);
+  const float* cb = P.coef + (int64_t)b * CK;
+  const float* db = P.d + (int64_t)b * CK;
+  const float c0 = tid < CK ? cb[tid] : 0.0f;
+  const float d0 = (SOFT && tid < CK) ? db[tid] : 0.0f;
+  float g0 = 0.0f;
+  if (tid < CL) g0 = P.jac[b * CL + tid] * (P.go_per_class ? P.go[b * CL + tid] : P.go[0]);
+  FastTile<C, VEC> ta, tb;
+  const uint32_t v0 = (uint32_t)(tid * VEC);
+  if (nsteps > 0) fast_load<T, C, VEC>(ta, xr, lr_, v0, SOFT);
+  treg.store(tabs, P.btab, P.rtab, n, nrepl);
+  if (tid < CK) {
+    scoef[tid] = c0;
+    if (SOFT) sdd[tid] = d0;
+  }
+  if (tid < CL) sg[tid] = g0;
+  for (int i = tid + kThreads; i < CK; i += kThreads) {
+    scoef[i] = cb[i];
+    if (SOFT) sdd[i] = db[i];
+  }
+  for (int i = tid + kThreads; i < CL; i += kThreads)
+    sg[i] = P.jac[b * CL + i] * (P.go_per_class ? P.go[b * CL + i] : P.go[0]);
+  __syncthreads();
+  const float* tab = tabs;
+  const float* repl = tabs + n + 2;
+
   if (nsteps > 0) {
-    FastTile<C, VEC> ta, tb;
-    const uint32_t v0 = (uint32_t)(tid * VEC);
-    fast_load<T, C, VEC>(ta, xr, lr_, v0, SOFT);
     for (int i = 0; i < nsteps; i += 2) {
       const uint32_t va = v0 + (uint32_t)(i * stride);
       const uint32_t vb = (i + 1 < nsteps) ? va + (uint32_t)stride : va;

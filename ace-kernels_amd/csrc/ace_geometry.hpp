@@ -12,6 +12,10 @@ constexpr int kFrac = 30;               // fixed-point fraction bits of the sums
 constexpr int kMaxChannels = 64;        // largest C with a built kernel
 constexpr size_t kMaxHistLds = 32 * 1024;  // default LDS budget of the histogram copies
 constexpr int kMaxCopyCount = 2047;        // hard: voxels one copy may count (11-bit field)
+constexpr int kCtrStride = 64;             // ints between ticket counters (one 256-byte line each)
+constexpr int kGroupTiles = 16;            // blocks per ticket group
+constexpr int kRepTiles = 256;             // blocks per replica of the final sums
+constexpr int kMaxReps = 4;                // replicas of the final sums per batch index
 
 // Channel variants with a compiled kernel: the kernel keeps C logits of VEC
 // voxels in registers.  EXACT variants fix C at compile time; the others
@@ -53,15 +57,16 @@ struct Geometry {
   int64_t tile_vox;    // voxels per block (one batch index)
   int64_t tiles;       // blocks per batch index
   int64_t nblk;        // total blocks
-  int64_t gs;          // blocks per reduction group
+  int64_t gs;          // blocks per ticket group
   int64_t gpb;         // groups per batch index
+  int reps;            // replicas of each batch index's final sums
   int copies;          // histogram copies (lane % copies)
+  int lchunk;          // log2 of the copies one lane adds in the block sums
   size_t tab_floats;   // padded bucket table (n + 2) + centre table (2K + 2)
   size_t lds_fwd;      // dynamic LDS of the forward kernel
   size_t lds_bwd;      // dynamic LDS of the backward kernel
-  int epi_batch;       // batch indices per epilogue pass
-  size_t ws_counters;  // bytes that must start zeroed (counters + final sums)
-  size_t off_fin, off_part, ws_bytes;
+  size_t off_fin;      // byte offset of the final sums in the workspace
+  size_t ws_bytes;     // workspace bytes; all of it starts zero and is left zero
 };
 
 // Blocks per batch index: aim for ~8 blocks per CU on a 256-CU part while
@@ -99,40 +104,40 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
     if (steps > max_steps) steps = (int)(max_steps > 0 ? max_steps : 1);
   }
   g.steps = steps;
+  // block sums: a lane adds up to 8 copies; hard packed words only as many as
+  // keep the count fields within kMaxCopyCount (a copy counts at most
+  // kThreads / copies lanes x steps x vec voxels)
+  const int64_t copy_vox = (int64_t)(kThreads / copies) * steps * g.var.vec;
+  int chunk = copies < 8 ? copies : 8;
+  while (chunk > 1 && !soft && chunk * copy_vox > kMaxCopyCount) chunk /= 2;
+  int lchunk = 0;
+  while ((1 << lchunk) < chunk) ++lchunk;
+  g.lchunk = lchunk;
   g.tile_vox = step_vox * steps;
   g.tiles = N > 0 ? cdiv(N, g.tile_vox) : 1;
   g.nblk = B * g.tiles;
-  // two-level reduction: groups of ~sqrt(tiles) blocks
-  int64_t gs = 1;
-  while (gs * gs < g.tiles) ++gs;
-  if (gs > 64) gs = 64;
-  g.gs = gs;
-  g.gpb = cdiv(g.tiles, gs);
+  // tickets: groups of kGroupTiles blocks, then the groups of a batch index;
+  // final sums replicated so that ~kRepTiles blocks share a replica
+  g.gs = g.tiles < kGroupTiles ? g.tiles : kGroupTiles;
+  g.gpb = cdiv(g.tiles, g.gs);
+  int64_t reps = cdiv(g.tiles, kRepTiles);
+  g.reps = (int)(reps > kMaxReps ? kMaxReps : reps);
   const int n = soft ? 2 * K : K;
   g.tab_floats = align_up((size_t)(n + 2) + (soft ? (size_t)(2 * K + 2) : 0), 4);
-  // the group-last block sums rows into 3 x CK u64 (LDS), and the last block
-  // reuses the histogram region for the epilogue: d, W, G, per-class f
-  // (float) and an empty flag per bin, for `epi_batch` batch indices at a time
+  // the epilogue block reuses the histogram region: d, W, G (float) and an
+  // empty flag per bin of one batch index, then 4 floats of the loss sum
   const size_t hist = align_up(per_copy * copies, 16);
-  const size_t acc = align_up((size_t)g.ck * 24, 16);
-  const size_t region = hist > acc ? hist : acc;
-  int64_t eb = (int64_t)(region / ((size_t)g.ck * 17));
-  if (eb < 1) eb = 1;
-  if (eb > B) eb = B;
-  g.epi_batch = (int)eb;
+  const size_t epi = align_up((size_t)g.ck * 13, 16);
+  const size_t region = hist > epi ? hist : epi;
   g.lds_fwd = g.tab_floats * 4 + region;
   // backward: tables + coef (+ d) + g
   g.lds_bwd = g.tab_floats * 4 + align_up((size_t)g.ck * (soft ? 2 : 1) + g.CL, 4) * 4;
-  // workspace: [ticket counters | final sums] must start zero and are left
-  // zero by every call; then the per-block partials
-  const int64_t counters = B * g.gpb + 1;
-  const size_t ctr_bytes = align_up((size_t)counters * sizeof(int), 256);
-  const size_t fin_bytes = align_up((size_t)B * 3 * g.ck * sizeof(unsigned long long), 256);
-  g.off_fin = ctr_bytes;
-  g.ws_counters = ctr_bytes + fin_bytes;
-  const size_t part_bytes = (size_t)g.nblk * 3 * g.ck * sizeof(long long);
-  g.off_part = g.ws_counters;
-  g.ws_bytes = align_up(g.off_part + part_bytes, 256);
+  // workspace: ticket counters (groups, batch indices, loss) and the final
+  // sums; it must start zero and every call leaves it zero
+  const int64_t counters = B * g.gpb + B + 1;
+  g.off_fin = align_up((size_t)counters * kCtrStride * sizeof(int), 256);
+  const size_t fin_bytes = (size_t)B * g.reps * 3 * g.ck * sizeof(unsigned long long);
+  g.ws_bytes = align_up(g.off_fin + fin_bytes, 256);
   return g;
 }
 

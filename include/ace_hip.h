@@ -66,14 +66,12 @@ const char* ace_error_string(int code);
 
 /*
  * Bytes of device workspace ace_forward needs for this problem.  The
- * workspace starts with a reset region (ticket counters and the final
- * fixed-point sums, `ace_workspace_reset_bytes()` bytes) followed by per-block
- * partial sums.  The reset region must be zero when a call starts; every call
- * leaves its own reset region zero again, so repeated calls on one problem
- * reuse a workspace without clearing.  A call whose reset region is larger
- * than the previous call's on the same buffer needs that region cleared first
- * (the previous call's partials may lie there).  Calls that share a workspace
- * must be ordered (same stream).
+ * workspace holds ticket counters and the final fixed-point sums; its first
+ * `ace_workspace_reset_bytes()` bytes (currently all of it) must be zero when
+ * a call starts, and every call leaves them zero again, so repeated calls
+ * reuse a workspace without clearing.  A call that needs more reset bytes than
+ * earlier calls on the same buffer have left zero needs the extra bytes
+ * cleared first.  Calls that share a workspace must be ordered (same stream).
  */
 size_t ace_workspace_bytes(int64_t batch, int64_t channels, int64_t voxels,
                            int num_bins, int binning, int x_dtype,

@@ -93,6 +93,47 @@ long long check_range(const float* table, int n, int right, float lo, float hi) 
   return bad;
 }
 
+// bucket<RIGHT, false> (no input clamp, the softmax path) at every float32 in
+// [lo, hi] within [0, 1], and at every float32 of [0, 1] within `ulps` of an
+// edge when ulps > 0 (lo, hi then ignored).
+long long check_unclamped(const float* table, int n, int right, float lo, float hi, int ulps) {
+  const std::vector<float> tab = padded(table, n);
+  auto one = [&](float p) -> long long {
+    int want = expected(table, n, p, right != 0);
+    if (want > n - 1) want = n - 1;
+    const int k = right ? ace::bucket<true, false>(p, (float)n, n, tab.data())
+                        : ace::bucket<false, false>(p, (float)n, n, tab.data());
+    return k != want ? 1 : 0;
+  };
+  long long bad = 0;
+  if (ulps > 0) {
+    std::vector<float> centres(table, table + n);
+    centres.push_back(0.0f);
+    centres.push_back(1.0f);
+    for (float c : centres) {
+      const int64_t b = (int64_t)to_bits(c);
+      for (int64_t d = -ulps; d <= ulps; ++d) {
+        const int64_t u = b + d;
+        if (u < 0 || u > (int64_t)to_bits(1.0f)) continue;
+        bad += one(from_bits((uint32_t)u));
+      }
+    }
+    return bad;
+  }
+  const uint32_t a = to_bits(lo), z = to_bits(hi);
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+  for (int64_t u = a; u <= (int64_t)z; ++u) bad += one(from_bits((uint32_t)u));
+  return bad;
+}
+
+// bucket<RIGHT, false> of a NaN (NaN logits) is 0, inside the histogram.
+int check_unclamped_nan(const float* table, int n) {
+  const std::vector<float> tab = padded(table, n);
+  const float q = std::nanf("");
+  return ace::bucket<false, false>(q, (float)n, n, tab.data()) == 0 &&
+         ace::bucket<true, false>(q, (float)n, n, tab.data()) == 0;
+}
+
 // Planted mistake for the sensitivity test: the first guess floor(p * n)
 // without the correction against the table.
 long long check_near_edges_uncorrected(const float* table, int n, int right, int ulps) {

@@ -11,7 +11,9 @@ against a binary search over the same float32 ``torch.linspace`` tables:
   hard (K edges) and soft (2K half boundaries), right = False / True;
 - every float32 in [0, 1 + eps32] (exhaustive) for the benchmark tables
   K = 20 and K = 50;
-- out-of-domain values (NaN, +-inf, > 1) stay inside [0, n - 1].
+- out-of-domain values (NaN, +-inf, > 1) stay inside [0, n - 1];
+- the softmax variant without input clamp (``bucket<RIGHT, false>``) on every
+  float32 of [0, 1] for K = 20 and 50, near every edge for every K, and NaN.
 """
 
 from __future__ import annotations
@@ -45,6 +47,11 @@ def harness(tmp_path_factory) -> ctypes.CDLL:
     lib.check_range.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float]
     lib.check_clamped.restype = ctypes.c_int
     lib.check_clamped.argtypes = [fp, ctypes.c_int]
+    lib.check_unclamped.restype = ctypes.c_longlong
+    lib.check_unclamped.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                    ctypes.c_int]
+    lib.check_unclamped_nan.restype = ctypes.c_int
+    lib.check_unclamped_nan.argtypes = [fp, ctypes.c_int]
     return lib
 
 
@@ -102,3 +109,22 @@ def test_edges_detect_an_uncorrected_index(harness) -> None:
         t = _table(k, False)
         total += harness.check_near_edges_uncorrected(_fp(t), t.size, 0, 8)
     assert total > 0
+
+
+@pytest.mark.parametrize("soft", [False, True])
+def test_unclamped_softmax_variant(harness, soft: bool) -> None:
+    """bucket<RIGHT, false>, used on softmax probabilities: exhaustive on [0, 1]
+    for the benchmark tables, near every edge for every K, NaN -> bin 0."""
+    for k in (20, 50):
+        t = _table(k, soft)
+        for right in (0, 1):
+            assert harness.check_unclamped(_fp(t), t.size, right, 0.0, 1.0, 0) == 0
+    bad = {}
+    for k in KS:
+        t = _table(k, soft)
+        for right in (0, 1):
+            n = harness.check_unclamped(_fp(t), t.size, right, 0.0, 0.0, 4096)
+            if n:
+                bad[(k, right)] = n
+        assert harness.check_unclamped_nan(_fp(t), t.size) == 1
+    assert not bad, bad
