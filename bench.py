@@ -6,17 +6,21 @@ One step = one forward + backward of the loss (``autograd.grad(loss.sum(),
 x)`` through the registry's ``hip_mi355x`` impl) on one batch of synthetic
 inputs already resident in HBM: configuration 2 (hard, B=2, C=4, 128^3
 fp32, int64 labels) for ``value``, configuration 3 (soft, same tensors)
-reported beside it.  Before every timed step a 1 GiB buffer is zeroed so
-that the 256 MB last-level cache starts cold (reference method:
-``src/ace_bench/timing.py:48-77``, with a flush larger than MI355X's cache).
-Each step is timed with HIP events on the stream the kernels run on; the
-median is reported, for eager execution and for a HIP-graph replay of the
-same step.
+reported beside it.  Before every launch -- warm-up included -- a 1 GiB
+buffer is read (summed), so that the inputs are not in the 256 MB last-level
+cache and the cache holds no dirty lines (reference method:
+``src/ace_bench/timing.py:48-77``, with a flush larger than MI355X's cache and
+reads instead of writes).  Each step is timed with HIP events on the stream the
+kernels run on; the median of eager execution is ``value`` (the reference's
+method, ``src/ace_bench/timing.py:48-77``); a HIP-graph replay of the same step
+is reported beside it, and forward and backward kernels are also timed alone.
 
-``roofline`` is for the dominant kernel, timed alone with events over K
-launches: achieved = its algorithmic bytes per launch / mean duration.
-``cpu_baseline`` times the reference algorithm (restated in ``oracle/``)
-fwd+bwd on configuration 1 on the host CPU.
+``roofline`` is for the dominant kernel: achieved = its algorithmic bytes per
+launch / its mean duration over the timed launches (events around each
+launch, cold cache).  ``traffic`` is read from the committed rocprofv3
+FETCH_SIZE / WRITE_SIZE summary when there is one.  ``cpu_baseline`` times the
+reference algorithm (restated in ``oracle/``) fwd+bwd on configuration 2 on
+the host CPU.
 
 Prints ONE JSON line (rank 0).  ``--gpus`` above 1 exits with a message: this
 build runs on one GPU.
@@ -40,6 +44,22 @@ for _p in (ROOT, ROOT / "ace-kernels_amd"):
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, 1 GB = 1e9 B
 METRIC = "fwd+bwd ms & % of HBM peak, B2 C4 128³ fp32, hard/soft binning"
 FLUSH_BYTES = 1 << 30
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_cfg2.json"
+
+
+class ReadFlush:
+    """Evicts the last-level cache by reading FLUSH_BYTES (clean lines only)."""
+
+    def __init__(self):
+        import torch
+
+        self.buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda")
+        self.out = torch.empty((), dtype=torch.float32, device="cuda")
+
+    def __call__(self) -> None:
+        import torch
+
+        torch.sum(self.buf, dim=0, out=self.out)
 
 
 def log(msg: str) -> None:
@@ -56,16 +76,18 @@ def _quantiles(ms):
 
 
 def time_steps(fn, steps: int, warmup: int, flush):
-    """Per-step event times (ms) of ``fn`` with a cache flush before each step."""
+    """Per-step event times (ms) of ``fn`` with a cache flush before each call
+    (warm-up calls too, so every launch of the kernels runs cold)."""
     import torch
 
     for _ in range(warmup):
+        flush()
         fn()
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     for s, e in zip(starts, ends):
-        flush.zero_()
+        flush()
         s.record()
         fn()
         e.record()
@@ -111,26 +133,31 @@ def bench_workload(wl, steps: int, warmup: int, flush):
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for _ in range(3):
+            flush()
             step()
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
         g_static = step()
+    flush()
     graph.replay()
     torch.cuda.synchronize()
+    flush()
     g_eager = step()
     torch.cuda.synchronize()
     graph_ok = bool(torch.equal(g_static, g_eager))
     graphed = time_steps(graph.replay, steps, warmup, flush)
 
-    # kernels alone, back to back (the roofline's per-launch duration)
+    # each kernel alone, cold (the roofline's per-launch duration)
     pl = hip.make_plan(x.detach(), y, cfg)
+    flush()
     loss, coef, d, jac, _, _ = hip.hip_forward(pl, cfg)
     go = torch.ones((), device="cuda")
-    fwd_ms = time_back_to_back(lambda: hip.hip_forward(pl, cfg), steps * 5, warmup)
-    bwd_ms = time_back_to_back(lambda: hip.hip_backward(pl, coef, d, jac, go), steps * 5, warmup)
     fwd_cold = time_steps(lambda: hip.hip_forward(pl, cfg), steps, warmup, flush)
+    bwd_cold = time_steps(lambda: hip.hip_backward(pl, coef, d, jac, go), steps, warmup, flush)
+    fwd_ms = statistics.fmean(fwd_cold)
+    bwd_ms = statistics.fmean(bwd_cold)
 
     n_vox = wl.batch * wl.voxels
     xb = wl.input_bytes()
@@ -146,17 +173,17 @@ def bench_workload(wl, steps: int, warmup: int, flush):
         "ideal_bytes_fwd": wl.ideal_bytes("fwd"),
         "graph_ms": _quantiles(graphed),
         "eager_ms": _quantiles(eager),
-        "fwd_kernel_ms_back_to_back": fwd_ms,
-        "bwd_kernel_ms_back_to_back": bwd_ms,
-        "fwd_ms_cold": _quantiles(fwd_cold)["p50"],
+        "fwd_ms": _quantiles(fwd_cold),
+        "bwd_ms": _quantiles(bwd_cold),
+        "fwd_GBps": wl.ideal_bytes("fwd") / (statistics.median(fwd_cold) * 1e-3) / 1e9,
         "graph_replay_matches_eager": graph_ok,
         "loss": float(loss.item()),
     }
-    p50 = out["graph_ms"]["p50"]
+    p50 = out["eager_ms"]["p50"]
     out["effective_GBps"] = ideal / (p50 * 1e-3) / 1e9
     out["pct_hbm_peak"] = 100.0 * out["effective_GBps"] / PEAK_HBM_GBPS
-    e50 = out["eager_ms"]["p50"]
-    out["eager_pct_hbm_peak"] = 100.0 * ideal / (e50 * 1e-3) / 1e9 / PEAK_HBM_GBPS
+    g50 = out["graph_ms"]["p50"]
+    out["graph_pct_hbm_peak"] = 100.0 * ideal / (g50 * 1e-3) / 1e9 / PEAK_HBM_GBPS
     kernels = {
         "ace_fwd": (fwd_ms, fwd_kernel_bytes, fwd_kernel_bytes / n_vox),
         "ace_bwd": (bwd_ms, bwd_kernel_bytes, bwd_kernel_bytes / n_vox),
@@ -169,13 +196,14 @@ def bench_workload(wl, steps: int, warmup: int, flush):
 
 
 def cpu_baseline(budget_s: float = 15.0):
-    """The reference algorithm (oracle restatement, torch CPU) fwd+bwd on cfg 1."""
+    """The reference algorithm (oracle restatement, torch CPU) fwd+bwd on the
+    benchmark workload (configuration 2), a bounded number of calls."""
     import torch
 
     from ace_kernels.workloads import workload
     from oracle.reference import reference_ace
 
-    wl = workload(1)
+    wl = workload(2)
     x, y = wl.make("cpu")
 
     def step():
@@ -200,7 +228,8 @@ def cpu_baseline(budget_s: float = 15.0):
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{wl.name}: reference loss (B x C bucketize/scatter loop + autograd) "
-                  f"fwd+bwd, {len(times)} calls p50, torch CPU intra-op threads",
+                  f"fwd+bwd, {len(times)} calls within {budget_s:.0f} s, p50, "
+                  f"torch CPU intra-op threads",
         "effective_GBps": ideal / (p50 * 1e-3) / 1e9,
         "host_cpu_count": os.cpu_count(),
     }
@@ -238,6 +267,17 @@ def profile_kernels(workloads, launches: int) -> None:
     log(f"copy kernel: {launches} x {src.numel() * 4} bytes read + written")
 
 
+def _traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` on configuration 2 from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy
+    kernel), or None when there is no summary."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+        return data[kernel]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -264,7 +304,7 @@ def main() -> int:
     if args.profile_kernels:
         profile_kernels([int(v) for v in args.workloads.split(",")], args.profile_kernels)
         return 0
-    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
+    flush = ReadFlush()
     results = []
     for idx in [int(v) for v in args.workloads.split(",")]:
         wl = workload(idx)
@@ -276,12 +316,12 @@ def main() -> int:
     achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
     line = {
         "metric": METRIC,
-        "value": main_r["graph_ms"]["p50"],
+        "value": main_r["eager_ms"]["p50"],
         "unit": "ms",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": main_r["graph_ms"]["p50"],
+        "ms_per_step": main_r["eager_ms"]["p50"],
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -291,12 +331,15 @@ def main() -> int:
             "workload": main_r["workload"],
             "binning": main_r["binning"],
             "shape": "B=2 C=4 128^3 fp32 logits, int64 labels, K=20",
-            "timing": "HIP-graph replay of autograd.grad(loss.sum(), x), p50 of per-step events, 1 GiB flush before each step",
+            "timing": "eager autograd.grad(loss.sum(), x) through ace_loss(impl='hip_mi355x'), "
+                      "p50 of per-step events, 1 GiB read flush before each step",
         },
+        "fwd_ms_p50": main_r["fwd_ms"]["p50"],
+        "bwd_ms_p50": main_r["bwd_ms"]["p50"],
         "pct_hbm_peak": main_r["pct_hbm_peak"],
         "effective_GBps": main_r["effective_GBps"],
-        "eager_ms_p50": main_r["eager_ms"]["p50"],
-        "eager_pct_hbm_peak": main_r["eager_pct_hbm_peak"],
+        "graph_ms_p50": main_r["graph_ms"]["p50"],
+        "graph_pct_hbm_peak": main_r["graph_pct_hbm_peak"],
         "roofline": {
             "bound": "hbm",
             "kernel": dom["kernel"],
@@ -304,9 +347,10 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBPS,
-            "traffic": None,
+            "traffic": _traffic(dom["kernel"]),
             "bytes_per_launch": dom["bytes"],
             "bytes_per_voxel": dom["bytes_per_voxel"],
+            "ms_mean": dom["ms"],
         },
         "workloads": results,
     }
