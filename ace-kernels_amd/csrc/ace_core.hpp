@@ -340,16 +340,19 @@ __device__ __forceinline__ void load_tables(float* lds, const float* btab, const
 
 // A thread's share of the LDS tables -- entries tid and tid + kThreads of the
 // padded bucket table and of the centre table -- held in registers, so that a
-// kernel can issue these loads, then its first tile's loads, and only then
-// wait for the tables (in-order vmcnt) and write them to LDS.
+// kernel can issue these loads, then its first tiles' loads, and only then
+// wait for the tables (in-order vmcnt, a partial wait) and write them to LDS.
+// The loads are unconditional (clamped in-bounds indices, unused values
+// discarded): a load under a branch would make the compiler wait for every
+// outstanding load instead.
 struct TableRegs {
-  float b[2], r[2];
+  float b[2], r[2];  // raw table values; padding applied when stored
   __device__ __forceinline__ void load(const float* btab, const float* rtab, int n, int nrepl) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int i = (int)threadIdx.x + u * kThreads;
-      b[u] = i == 0 ? -__builtin_inff() : (i <= n ? btab[i - 1] : __builtin_inff());
-      r[u] = i < nrepl ? rtab[i] : 0.0f;
+      b[u] = btab[min(max(i - 1, 0), n - 1)];
+      r[u] = nrepl > 0 ? rtab[min(i, nrepl - 1)] : 0.0f;
     }
   }
   __device__ __forceinline__ void store(float* lds, const float* btab, const float* rtab, int n,
@@ -357,7 +360,7 @@ struct TableRegs {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int i = (int)threadIdx.x + u * kThreads;
-      if (i < n + 2) lds[i] = b[u];
+      if (i < n + 2) lds[i] = i == 0 ? -__builtin_inff() : (i <= n ? b[u] : __builtin_inff());
       if (i < nrepl) lds[n + 2 + i] = r[u];
     }
     // tables longer than 2 x kThreads entries
@@ -961,6 +964,11 @@ __device__ __forceinline__ unsigned long long* bin_at(unsigned long long* base, 
                                                ((uint32_t)k << lsh));
 }
 
+// Load source of the pipelined kernels' first two steps when a tile has no
+// full step: 64 bytes of zeros in device memory (read, never used), so that
+// these loads can be issued unconditionally.
+static __device__ __align__(16) unsigned char g_dummy_src[64];
+
 template <int C, int VEC>
 struct FastTile {
   float x[C][VEC];
@@ -1142,7 +1150,23 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   treg.load(P.btab, P.rtab, n, nrepl);
   FastTile<C, VEC> ta, tb;
   const uint32_t v0 = (uint32_t)(tid * VEC);
-  if (nsteps > 0) fast_load<T, C, VEC>(ta, xr, lr_, v0, true);
+  // voxel offset of this lane in step j, clamped to the last step: a load
+  // past the end (odd step counts only) re-reads the last step (L2 hit) so
+  // that every load is unconditional and the waits stay partial
+  auto at = [&](int j) -> uint32_t {
+    return v0 + (uint32_t)((j < nsteps ? j : nsteps - 1) * stride);
+  };
+  {
+    // unconditional (a load under a branch would turn the table wait below
+    // into a wait for every load); without a full step they read g_dummy_src
+    const bool pipe = nsteps > 0;
+    const T* px[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) px[c] = pipe ? xr[c] : reinterpret_cast<const T*>(g_dummy_src);
+    const long long* pl = pipe ? lr_ : reinterpret_cast<const long long*>(g_dummy_src);
+    fast_load<T, C, VEC>(ta, px, pl, pipe ? at(0) : 0u, true);
+    fast_load<T, C, VEC>(tb, px, pl, pipe ? at(1) : 0u, true);
+  }
   treg.store(tabs, P.btab, P.rtab, n, nrepl);
   {
     unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
@@ -1157,16 +1181,18 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   for (int c = 0; c < C; ++c)
     hb[c] = H.a + ((size_t)((c < off ? 0 : c - off) * K) << lr) + copy;
 
+  // two tiles in rotation (steps i and i + 1 loaded before step i is
+  // binned); the last pair is peeled so that no step is loaded twice
   if (nsteps > 0) {
-    for (int i = 0; i < nsteps; i += 2) {
-      const uint32_t va = v0 + (uint32_t)(i * stride);
-      const uint32_t vb = (i + 1 < nsteps) ? va + (uint32_t)stride : va;
-      fast_load<T, C, VEC>(tb, xr, lr_, vb, true);
+    int i = 0;
+    for (; i + 2 < nsteps; i += 2) {
       fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, skip0, lsh, hb, words);
-      const uint32_t vc = (i + 2 < nsteps) ? va + 2u * (uint32_t)stride : vb;
-      fast_load<T, C, VEC>(ta, xr, lr_, vc, true);
-      if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, skip0, lsh, hb, words);
+      fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), true);
+      fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, skip0, lsh, hb, words);
+      fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), true);
     }
+    fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, skip0, lsh, hb, words);
+    if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, skip0, lsh, hb, words);
   }
   // remaining full vectors (not every thread has one), then single voxels
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
@@ -1265,13 +1291,26 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   treg.load(P.btab, P.rtab, n, nrepl);
   const float* cb = P.coef + (int64_t)b * CK;
   const float* db = P.d + (int64_t)b * CK;
-  const float c0 = tid < CK ? cb[tid] : 0.0f;
-  const float d0 = (SOFT && tid < CK) ? db[tid] : 0.0f;
-  float g0 = 0.0f;
-  if (tid < CL) g0 = P.jac[b * CL + tid] * (P.go_per_class ? P.go[b * CL + tid] : P.go[0]);
+  // unconditional loads (clamped indices) so that the waits below stay partial
+  const int tc_ = min(tid, CK - 1);
+  const int tl_ = min(tid, CL - 1);
+  const float c0 = cb[tc_];
+  const float d0 = SOFT ? db[tc_] : 0.0f;
+  const float g0 = P.jac[b * CL + tl_] * P.go[P.go_per_class ? b * CL + tl_ : 0];
   FastTile<C, VEC> ta, tb;
   const uint32_t v0 = (uint32_t)(tid * VEC);
-  if (nsteps > 0) fast_load<T, C, VEC>(ta, xr, lr_, v0, SOFT);
+  auto at = [&](int j) -> uint32_t {
+    return v0 + (uint32_t)((j < nsteps ? j : nsteps - 1) * stride);
+  };
+  {
+    const bool pipe = nsteps > 0;
+    const T* px[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) px[c] = pipe ? xr[c] : reinterpret_cast<const T*>(g_dummy_src);
+    const long long* pl = pipe ? lr_ : reinterpret_cast<const long long*>(g_dummy_src);
+    fast_load<T, C, VEC>(ta, px, pl, pipe ? at(0) : 0u, SOFT);
+    fast_load<T, C, VEC>(tb, px, pl, pipe ? at(1) : 0u, SOFT);
+  }
   treg.store(tabs, P.btab, P.rtab, n, nrepl);
   if (tid < CK) {
     scoef[tid] = c0;
@@ -1288,21 +1327,27 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   const float* tab = tabs;
   const float* repl = tabs + n + 2;
 
+  // two tiles in rotation (steps i and i + 1 loaded before step i is
+  // processed); the last pair is peeled so that no step is loaded twice
   if (nsteps > 0) {
-    for (int i = 0; i < nsteps; i += 2) {
-      const uint32_t va = v0 + (uint32_t)(i * stride);
-      const uint32_t vb = (i + 1 < nsteps) ? va + (uint32_t)stride : va;
-      fast_load<T, C, VEC>(tb, xr, lr_, vb, SOFT);
+    int i = 0;
+    for (; i + 2 < nsteps; i += 2) {
       fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, repl, scoef, sdd, sg, K, off);
 #pragma unroll
-      for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + va, ta.x[c]);
-      const uint32_t vc = (i + 2 < nsteps) ? va + 2u * (uint32_t)stride : vb;
-      fast_load<T, C, VEC>(ta, xr, lr_, vc, SOFT);
-      if (i + 1 < nsteps) {
-        fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, repl, scoef, sdd, sg, K, off);
+      for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i), ta.x[c]);
+      fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), SOFT);
+      fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, repl, scoef, sdd, sg, K, off);
 #pragma unroll
-        for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + vb, tb.x[c]);
-      }
+      for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i + 1), tb.x[c]);
+      fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), SOFT);
+    }
+    fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, repl, scoef, sdd, sg, K, off);
+#pragma unroll
+    for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i), ta.x[c]);
+    if (i + 1 < nsteps) {
+      fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, repl, scoef, sdd, sg, K, off);
+#pragma unroll
+      for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i + 1), tb.x[c]);
     }
   }
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
