@@ -109,6 +109,17 @@ int check_common(const void* x, int x_dtype, const void* target, int target_kind
 
 int to_code(hipError_t e) { return e == hipSuccess ? ACE_OK : ACE_EHIP + (int)e; }
 
+// The activation is not an argument here: size for the larger layout (soft
+// moments when the channel count has a fast kernel and targets are labels).
+Geometry workspace_geometry(int64_t batch, int64_t channels, int64_t voxels, int num_bins,
+                            int binning, int include_background, int target_kind) {
+  const bool soft = binning == ACE_SOFT;
+  const bool labels = target_kind == ACE_TARGET_LABELS_I64;
+  return make_geometry(batch, channels, voxels, num_bins, soft, include_background != 0, labels,
+                       env_steps("ACE_FWD_STEPS"), env_copies(),
+                       soft && labels && fast_channels(channels));
+}
+
 }  // namespace
 }  // namespace ace
 
@@ -134,23 +145,20 @@ size_t ace_workspace_bytes(int64_t batch, int64_t channels, int64_t voxels, int 
                            int binning, int x_dtype, int include_background, int target_kind) {
   (void)x_dtype;
   if (batch < 1 || channels < 1 || voxels < 0 || num_bins < 1) return 0;
-  const Geometry g = make_geometry(batch, channels, voxels, num_bins, binning == ACE_SOFT,
+  const Geometry g = workspace_geometry(batch, channels, voxels, num_bins, binning,
+                                        include_background, target_kind);
+  const Geometry h = make_geometry(batch, channels, voxels, num_bins, binning == ACE_SOFT,
                                    include_background != 0,
                                    target_kind == ACE_TARGET_LABELS_I64,
                                    env_steps("ACE_FWD_STEPS"), env_copies());
-  return g.ws_bytes;
+  return g.ws_bytes > h.ws_bytes ? g.ws_bytes : h.ws_bytes;
 }
 
 size_t ace_workspace_reset_bytes(int64_t batch, int64_t channels, int64_t voxels,
                                  int num_bins, int binning, int x_dtype,
                                  int include_background, int target_kind) {
-  (void)x_dtype;
-  if (batch < 1 || channels < 1 || voxels < 0 || num_bins < 1) return 0;
-  const Geometry g = make_geometry(batch, channels, voxels, num_bins, binning == ACE_SOFT,
-                                   include_background != 0,
-                                   target_kind == ACE_TARGET_LABELS_I64,
-                                   env_steps("ACE_FWD_STEPS"), env_copies());
-  return g.ws_bytes;
+  return ace_workspace_bytes(batch, channels, voxels, num_bins, binning, x_dtype,
+                             include_background, target_kind);
 }
 
 int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
@@ -169,9 +177,12 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   if (reduction != ACE_RED_NONE && !loss) return ACE_EINVAL;
   const bool soft = binning == ACE_SOFT;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
+  const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
+  // soft + softmax + labels on a fast channel count: the moments kernels
+  const bool moments = soft && labels && act == kActSoftmax && fast_channels(channels);
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
                                    include_background != 0, labels, env_steps("ACE_FWD_STEPS"),
-                                   env_copies());
+                                   env_copies(), moments);
   if (workspace_bytes < g.ws_bytes) return ACE_EWORKSPACE;
   if (g.lds_fwd > kMaxLds) return ACE_EUNSUPPORTED;
   if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
@@ -193,7 +204,7 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   p.C = (int)channels;
   p.off = g.off;
   p.K = num_bins;
-  p.act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
+  p.act = act;
   p.tk = labels ? kTgtLabels : kTgtOnehot;
   p.copies = g.copies;
   p.vec_ok = vec_ok ? 1 : 0;
@@ -231,8 +242,11 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   if (!coef || !jac || !grad_output || !dx) return ACE_EINVAL;
   if (soft && !diff) return ACE_EINVAL;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
+  const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
+  const bool moments = soft && labels && act == kActSoftmax && fast_channels(channels);
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
-                                   include_background != 0, labels, env_steps("ACE_BWD_STEPS"));
+                                   include_background != 0, labels, env_steps("ACE_BWD_STEPS"), 0,
+                                   moments);
   if (g.lds_bwd > kMaxLds) return ACE_EUNSUPPORTED;
   if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
   if (voxels == 0) return ACE_OK;
@@ -254,7 +268,7 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   p.C = (int)channels;
   p.off = g.off;
   p.K = num_bins;
-  p.act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
+  p.act = act;
   p.tk = labels ? kTgtLabels : kTgtOnehot;
   p.vec_ok = vec_ok ? 1 : 0;
   p.go_per_class = grad_output_per_class != 0;

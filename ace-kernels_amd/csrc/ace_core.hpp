@@ -404,10 +404,13 @@ struct Tile {
 // LDS views of one block's histogram copies.
 struct Hist {
   unsigned long long* a;  // hard: packed count | label count | sum p   [CK][R]
+                          // moments: the same per half-bin            [2CK][R]
   long long* g1;          // hard + per-channel targets: sum y          [CK][R]
   long long* w;           // soft: sum of weights                       [CK][R]
   long long* p;           // soft: sum of weight * p                    [CK][R]
   long long* g;           // soft: sum of weight * y                    [CK][R]
+  unsigned long long* m2; // moments: sum p^2                           [2CK][R]
+  unsigned long long* mg; // moments: sum p over the labelled voxels    [2CK][R]
 };
 
 // Adds NV voxels (logits xv, labels lab or targets yv) into the histograms.
@@ -495,41 +498,111 @@ __device__ __forceinline__ int* counter(const FwdParams& P, int64_t i) {
 // Epilogue of batch index b (kernels/epilogue.py:23-82): final sums -> d, W,
 // G per bin; per class row: K_ne, f, coef, jac.  Runs in the block that drew
 // the last ticket of batch b; it also leaves b's final sums zero.
-template <bool SOFT>
-__device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char* hist, int CK,
-                                               int CL, int b) {
+// Soft moments: the bin sums of half-bin h (interval of half boundaries
+// between the replicated centres cl = repl[h] and cr = repl[h + 2]) follow
+// from its moments, because both interpolation weights are linear in p there:
+// lw = (cr - p) / S, rw = (p - cl) / S with S = cr - cl (common.py:43-61), so
+//   W_l += (cr n - S1) / S,   W_r += (S1 - cl n) / S,
+//   P_l += (cr S1 - S2) / S,  P_r += (S2 - cl S1) / S,
+//   G_l += (cr g - Sg) / S,   G_r += (Sg - cl g) / S
+// with n = count, S1 = sum p, S2 = sum p^2, g = labelled count, Sg = sum p
+// over the labelled voxels; bins l = max(h-1,0)/2, r = min(h+1,2K-1)/2.  The
+// weights are the exact-arithmetic ones (the reference rounds ld, rd and S to
+// float32 per voxel: a ~1e-7 relative difference per voxel).
+__device__ __forceinline__ void moment_terms(double n, double g, double s1, double s2, double sg,
+                                             double cl, double cr, double* out) {
+  const double S = cr - cl;
+  out[0] = (cr * n - s1) / S;
+  out[1] = (s1 - cl * n) / S;
+  out[2] = (cr * s1 - s2) / S;
+  out[3] = (s2 - cl * s1) / S;
+  out[4] = (cr * g - sg) / S;
+  out[5] = (sg - cl * g) / S;
+}
+
+template <bool SOFT, bool MOM>
+__device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char* hist,
+                                               const float* repl, int CK, int CL, int b) {
   const int tid = threadIdx.x;
   const int K = P.K;
-  const int W3 = 3 * CK;
+  const int NV = fin_values(CK, MOM);
   const int reps = P.reps;
   float* sd = reinterpret_cast<float*>(hist);
   float* sw = sd + CK;
   float* sg = sw + CK;
   unsigned char* se = reinterpret_cast<unsigned char*>(sg + CK);
-  unsigned long long* fb = P.fin + (int64_t)b * reps * W3;
+  unsigned long long* fb = P.fin + (int64_t)b * reps * NV;
   const int64_t BCK = (int64_t)P.B * CK;
   const double dscale = 1.0 / 1073741824.0;
-  for (int t = tid; t < CK; t += kThreads) {
-    // every replica's three sums in flight at once (reps <= kMaxReps)
-    long long s0 = 0, s1 = 0, s2 = 0;
+  double* terms = reinterpret_cast<double*>(hist + 16 * (size_t)CK);  // [2CK][6]
+  if constexpr (MOM) {
+    // per half-bin: the five moments (every replica in flight at once), then
+    // its six contributions
+    const int H2 = 2 * CK;
+    for (int t = tid; t < H2; t += kThreads) {
+      long long m[5] = {0, 0, 0, 0, 0};
 #pragma unroll
-    for (int r = 0; r < kMaxReps; ++r) {
-      if (r < reps) {
-        unsigned long long* f = fb + (int64_t)r * W3;
-        s0 += (long long)load_dev(&f[t]);
-        s1 += (long long)load_dev(&f[CK + t]);
-        s2 += (long long)load_dev(&f[2 * CK + t]);
+      for (int r = 0; r < kMaxReps; ++r) {
+        if (r < reps) {
+          unsigned long long* f = fb + (int64_t)r * NV;
+#pragma unroll
+          for (int v = 0; v < 5; ++v) m[v] += (long long)load_dev(&f[v * H2 + t]);
+        }
       }
+      for (int r = 0; r < reps; ++r) {
+        unsigned long long* f = fb + (int64_t)r * NV;
+#pragma unroll
+        for (int v = 0; v < 5; ++v) store_dev(&f[v * H2 + t], 0ull);
+      }
+      const int hh = t % (2 * K);
+      moment_terms((double)m[0], (double)m[1], (double)m[2] * dscale, (double)m[3] * dscale,
+                   (double)m[4] * dscale, (double)repl[hh], (double)repl[hh + 2], terms + 6 * t);
     }
-    for (int r = 0; r < reps; ++r) {
-      unsigned long long* f = fb + (int64_t)r * W3;
-      store_dev(&f[t], 0ull);
-      store_dev(&f[CK + t], 0ull);
-      store_dev(&f[2 * CK + t], 0ull);
+    __syncthreads();
+  }
+  for (int t = tid; t < CK; t += kThreads) {
+    double Wd, Pd, Gd;
+    if constexpr (MOM) {
+      // bin k of channel row cl: left share of half-bins l(h) = k, right share
+      // of r(h) = k, h in [2k - 1, 2k + 2], in increasing h
+      const int cl = t / K;
+      const int k = t - cl * K;
+      const double* tb = terms + 6 * (size_t)(cl * 2 * K);
+      Wd = Pd = Gd = 0.0;
+      for (int hh = max(2 * k - 1, 0); hh <= min(2 * k + 2, 2 * K - 1); ++hh) {
+        if ((max(hh - 1, 0) >> 1) == k) {
+          Wd += tb[6 * hh];
+          Pd += tb[6 * hh + 2];
+          Gd += tb[6 * hh + 4];
+        }
+        if ((min(hh + 1, 2 * K - 1) >> 1) == k) {
+          Wd += tb[6 * hh + 1];
+          Pd += tb[6 * hh + 3];
+          Gd += tb[6 * hh + 5];
+        }
+      }
+    } else {
+      // every replica's three sums in flight at once (reps <= kMaxReps)
+      long long s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+      for (int r = 0; r < kMaxReps; ++r) {
+        if (r < reps) {
+          unsigned long long* f = fb + (int64_t)r * NV;
+          s0 += (long long)load_dev(&f[t]);
+          s1 += (long long)load_dev(&f[CK + t]);
+          s2 += (long long)load_dev(&f[2 * CK + t]);
+        }
+      }
+      for (int r = 0; r < reps; ++r) {
+        unsigned long long* f = fb + (int64_t)r * NV;
+        store_dev(&f[t], 0ull);
+        store_dev(&f[CK + t], 0ull);
+        store_dev(&f[2 * CK + t], 0ull);
+      }
+      Wd = (double)s0 * dscale;
+      Pd = (double)s1 * dscale;
+      Gd = (double)s2 * dscale;
     }
-    const double Wd = (double)s0 * dscale;
-    const double Pd = (double)s1 * dscale;
-    const double Gd = (double)s2 * dscale;
     const int64_t o = (int64_t)b * CK + t;
     if (P.stats) {
       P.stats[o] = Wd;
@@ -592,6 +665,52 @@ __device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char
 // the Q lanes combine with shuffles and the first one issues the atomics, so
 // one wave request covers 64 / Q consecutive bins.  The copy index is skewed
 // by the bin so that the lanes of a wave read distinct bank pairs.
+// Moments variant: 5 values per half-bin (count, labelled count, sum p,
+// sum p^2, labelled sum p; the counts unscaled), fin layout [5][2CK].
+__device__ __forceinline__ void block_moments(const FwdParams& P, const Hist& H, int CK,
+                                              unsigned long long* fin) {
+  const int tid = threadIdx.x;
+  const int R = P.copies;
+  const int chunk = 1 << P.lchunk;
+  const int lq = __builtin_ctz((unsigned)R) - P.lchunk;
+  const int Q = 1 << lq;
+  const int H2 = 2 * CK;
+  const int total = H2 << lq;
+  for (int base = 0; base < total; base += kThreads) {
+    const int i = base + tid;
+    const int t = i >> lq;
+    const int part = i & (Q - 1);
+    long long m[5] = {0, 0, 0, 0, 0};
+    if (t < H2) {
+      const int w0 = t * R + part * chunk;
+      unsigned long long a = 0, q2 = 0, qg = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < chunk) {
+          const int w = w0 + ((j + t) & (chunk - 1));
+          a += H.a[w];
+          q2 += H.m2[w];
+          qg += H.mg[w];
+        }
+      }
+      const unsigned long long hi = (a + (1ull << (kShiftG - 1))) >> kShiftG;
+      m[0] = (long long)(hi >> (kShiftN - kShiftG));
+      m[1] = (long long)(hi & ((1ull << (kShiftN - kShiftG)) - 1));
+      m[2] = (long long)(a - (hi << kShiftG));
+      m[3] = (long long)q2;
+      m[4] = (long long)qg;
+    }
+#pragma unroll
+    for (int v = 0; v < 5; ++v)
+      for (int o = 1; o < Q; o <<= 1) m[v] += __shfl_xor(m[v], o, 64);
+    if (t < H2 && part == 0) {
+#pragma unroll
+      for (int v = 0; v < 5; ++v)
+        if (m[v]) atomicAdd(&fin[v * H2 + t], (unsigned long long)m[v]);
+    }
+  }
+}
+
 template <bool SOFT>
 __device__ __forceinline__ void block_sums(const FwdParams& P, const Hist& H, int CK, bool labels,
                                            unsigned long long* fin) {
@@ -654,12 +773,17 @@ __device__ __forceinline__ void block_sums(const FwdParams& P, const Hist& H, in
 // pick the last block of each group of gs tiles, the last group of batch b
 // (which runs b's epilogue) and the last batch (which sums the per-class
 // errors into the loss in a fixed order).
-template <bool SOFT>
+template <bool SOFT, bool MOM>
 __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, unsigned char* hist,
-                                           int CK, int CL, int b, int64_t tile, bool labels) {
+                                           const float* repl, int CK, int CL, int b,
+                                           int64_t tile, bool labels) {
   const int tid = threadIdx.x;
-  const int W3 = 3 * CK;
-  block_sums<SOFT>(P, H, CK, labels, P.fin + ((int64_t)b * P.reps + tile % P.reps) * W3);
+  unsigned long long* fin =
+      P.fin + ((int64_t)b * P.reps + tile % P.reps) * fin_values(CK, MOM);
+  if constexpr (MOM)
+    block_moments(P, H, CK, fin);
+  else
+    block_sums<SOFT>(P, H, CK, labels, fin);
   __shared__ int s_last;
   wait_own_writes();
   __syncthreads();
@@ -678,7 +802,7 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
   }
   __syncthreads();
   if (!s_last) return;
-  batch_epilogue<SOFT>(P, hist, CK, CL, b);
+  batch_epilogue<SOFT, MOM>(P, hist, repl, CK, CL, b);
   if (P.red == kRedNone) return;
 
   // ---- loss: the last batch epilogue sums the B x C' per-class errors
@@ -786,7 +910,7 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
     fwd_accumulate<CMAX, EXACT, 1, SOFT, RIGHT>(P, H, btab, repl, nc, copy, xv, lab, yv, labels);
   }
   __syncthreads();
-  fwd_finish<SOFT>(P, H, hist, CK, CL, b, tile, labels);
+  fwd_finish<SOFT, false>(P, H, hist, repl, CK, CL, b, tile, labels);
 }
 
 // ------------------------------------------------------------ backward
@@ -1073,31 +1197,30 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
         lds_add(bin_at(hb[c], k, lsh), ((unsigned long long)hi << 32) | q);
       }
     } else {
-      unsigned long long* gl = hb[0];
-      unsigned long long* gr = hb[0];
-      uint32_t glw = 0u, grw = 0u;
+      // soft: moments of the voxel's half-bin h (count | labelled count |
+      // sum p packed as in hard binning, sum p^2, labelled sum p)
+      unsigned long long* ga = hb[0];
+      uint32_t gq = 0u;
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         if (c == 0 && skip0) continue;
-        const SoftW w = soft_assign<RIGHT, false>(p[c], K, nf, tab, repl);
-        unsigned long long* sl = bin_at(hb[c], w.l, lsh);
-        unsigned long long* sr = bin_at(hb[c], w.r, lsh);
-        const uint32_t ql = (uint32_t)rintf(w.lw * 1073741824.0f);
-        const uint32_t qr = (uint32_t)rintf(w.rw * 1073741824.0f);
-        lds_add(sl, (unsigned long long)ql);
-        lds_add(sr, (unsigned long long)qr);
-        lds_add(sl + words, (unsigned long long)(uint32_t)rintf((w.lw * p[c]) * 1073741824.0f));
-        lds_add(sr + words, (unsigned long long)(uint32_t)rintf((w.rw * p[c]) * 1073741824.0f));
+        const int h = bucket<RIGHT, false>(p[c], nf, 2 * K, tab);
+        const uint32_t q = (uint32_t)rintf(p[c] * 1073741824.0f);
+        // the square of the quantised p (q 2^-30), exact in 64 bits, rounded
+        // to the same fixed point: the moments then describe one set of
+        // values (a float32 p * p would carry a 2^-24 relative error that the
+        // moment formulas amplify by 1 / S)
+        const uint32_t q2 = (uint32_t)(((unsigned long long)q * q + (1ull << 29)) >> 30);
         const bool hit = lab == (uint32_t)c;
-        gl = hit ? sl : gl;
-        gr = hit ? sr : gr;
-        glw = hit ? ql : glw;
-        grw = hit ? qr : grw;
+        const uint32_t hi = hit ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
+                                : (1u << (kShiftN - 32));
+        unsigned long long* a = bin_at(hb[c], h, lsh);
+        lds_add(a, ((unsigned long long)hi << 32) | q);
+        lds_add(a + words, (unsigned long long)q2);
+        ga = hit ? a : ga;
+        gq = hit ? q : gq;
       }
-      if (lab != 0xffffffffu && !(lab == 0u && skip0)) {
-        lds_add(gl + 2 * words, (unsigned long long)glw);
-        lds_add(gr + 2 * words, (unsigned long long)grw);
-      }
+      if (lab != 0xffffffffu && !(lab == 0u && skip0)) lds_add(ga + 2 * words, (unsigned long long)gq);
     }
   }
 }
@@ -1122,13 +1245,14 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
 
   const size_t tab_floats = (size_t)(((n + 2) + (SOFT ? 2 * K + 2 : 0) + 3) / 4 * 4);
   unsigned char* hist = smem + tab_floats * 4;
+  // bins per channel: K (hard) or 2K half-bins (soft moments)
+  const int NB = SOFT ? 2 * K : K;
+  const size_t words = (size_t)CL * NB * R;  // u64 words of one histogram array
   Hist H;
   H.a = reinterpret_cast<unsigned long long*>(hist);
-  H.g1 = reinterpret_cast<long long*>(hist) + (size_t)CK * R;
-  H.w = reinterpret_cast<long long*>(hist);
-  H.p = H.w + (size_t)CK * R;
-  H.g = H.p + (size_t)CK * R;
-  const size_t hist_words = (hist_bytes_per_copy(CK, SOFT, true) * (size_t)R + 7) / 8;
+  H.m2 = H.a + words;
+  H.mg = H.a + 2 * words;
+  const size_t hist_words = (hist_bytes_per_copy(CK, SOFT, true, SOFT) * (size_t)R + 7) / 8;
   const int nrepl = SOFT ? 2 * K + 2 : 0;
 
   const int64_t N = P.N;
@@ -1139,7 +1263,6 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   for (int c = 0; c < C; ++c)
     xr[c] = reinterpret_cast<const T*>(P.x) + ((int64_t)b * C + c) * N + t0;
   const long long* lr_ = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
-  const size_t words = (size_t)CK * R;
   const int nfull = P.vec_ok ? nvox / VEC * VEC : 0;
   const int stride = kThreads * VEC;
   const int nsteps = nfull / stride;  // steps in which every thread has a full vector
@@ -1179,7 +1302,7 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   unsigned long long* hb[C];
 #pragma unroll
   for (int c = 0; c < C; ++c)
-    hb[c] = H.a + ((size_t)((c < off ? 0 : c - off) * K) << lr) + copy;
+    hb[c] = H.a + ((size_t)((c < off ? 0 : c - off) * NB) << lr) + copy;
 
   // two tiles in rotation (steps i and i + 1 loaded before step i is
   // binned); the last pair is peeled so that no step is loaded twice
@@ -1206,15 +1329,38 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
     fast_accumulate<C, 1, SOFT, RIGHT>(t, tab, repl, K, skip0, lsh, hb, words);
   }
   __syncthreads();
-  fwd_finish<SOFT>(P, H, hist, CK, CL, b, tile, true);
+  fwd_finish<SOFT, SOFT>(P, H, hist, repl, CK, CL, b, tile, true);
+}
+
+// Soft backward per half-bin: with the exact-arithmetic weights of the
+// moments forward (lw = (cr - p) / S, rw = (p - cl) / S, S = cr - cl), the
+// soft dL/dp of v2_autograd.py:94-104,
+//   g (coef_l (lw - (p - y - d_l) / S) + coef_r (rw + (p - y - d_r) / S)),
+// is linear in p and y: g/S (coef_l (cr + d_l) - coef_r (cl + d_r))
+// + 2 g/S (coef_r - coef_l) (p - y/2).  sab[2h], sab[2h + 1] hold the two
+// coefficients (computed in float64) for half-bin h of every loss channel.
+__device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const float* repl,
+                                                           const float* scoef, const float* sdd,
+                                                           const float* sg, int K, int CL) {
+  const int H = 2 * K;
+  for (int t = threadIdx.x; t < CL * H; t += kThreads) {
+    const int cl = t / H;
+    const int hh = t - cl * H;
+    const int l = max(hh - 1, 0) >> 1;
+    const int r = min(hh + 1, H - 1) >> 1;
+    const double cL = repl[hh], cR = repl[hh + 2];
+    const double gs = (double)sg[cl] / (cR - cL);
+    const double kl = scoef[cl * K + l], kr = scoef[cl * K + r];
+    sab[2 * t] = (float)(gs * (kl * (cR + (double)sdd[cl * K + l]) - kr * (cL + (double)sdd[cl * K + r])));
+    sab[2 * t + 1] = (float)(2.0 * gs * (kr - kl));
+  }
 }
 
 // Backward of one tile, in place in t.x (logits in, gradient out).
 template <int C, int VEC, bool SOFT, bool RIGHT>
 __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* tab,
-                                              const float* repl, const float* scoef,
-                                              const float* sdd, const float* sg, int K,
-                                              int off) {
+                                              const float* sab, const float* scoef,
+                                              const float* sg, int K, int off) {
   const float nf = (float)(SOFT ? 2 * K : K);
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
@@ -1234,12 +1380,10 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
         const int k = bucket<RIGHT, false>(p[c], nf, K, tab);
         gp[c] = scoef[cl * K + k] * sg[cl];
       } else {
-        const SoftW w = soft_assign<RIGHT, false>(p[c], K, nf, tab, repl);
-        const float y = lab == (uint32_t)c ? 1.0f : 0.0f;
-        const float resid = p[c] - y;
-        const float left = scoef[cl * K + w.l] * (w.lw - w.inv_span * (resid - sdd[cl * K + w.l]));
-        const float rght = scoef[cl * K + w.r] * (w.rw + w.inv_span * (resid - sdd[cl * K + w.r]));
-        gp[c] = sg[cl] * (left + rght);
+        const int h = bucket<RIGHT, false>(p[c], nf, 2 * K, tab);
+        const float2 ab = *reinterpret_cast<const float2*>(sab + 2 * (cl * 2 * K + h));
+        const float y = lab == (uint32_t)c ? 0.5f : 0.0f;
+        gp[c] = fmaf(ab.y, p[c] - y, ab.x);
       }
     }
     float dot = 0.0f;
@@ -1268,6 +1412,8 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   float* scoef = tabs + tab_floats;
   float* sdd = scoef + CK;
   float* sg = sdd + (SOFT ? CK : 0);
+  // soft: (A, B) per half-bin, 8-byte aligned after g
+  float* sab = sg + ((CL + 1) & ~1);
   const int nrepl = SOFT ? 2 * K + 2 : 0;
 
   const int64_t N = P.N;
@@ -1326,26 +1472,30 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   __syncthreads();
   const float* tab = tabs;
   const float* repl = tabs + n + 2;
+  if constexpr (SOFT) {
+    soft_half_bin_coefficients(sab, repl, scoef, sdd, sg, K, CL);
+    __syncthreads();
+  }
 
   // two tiles in rotation (steps i and i + 1 loaded before step i is
   // processed); the last pair is peeled so that no step is loaded twice
   if (nsteps > 0) {
     int i = 0;
     for (; i + 2 < nsteps; i += 2) {
-      fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, repl, scoef, sdd, sg, K, off);
+      fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, sab, scoef, sg, K, off);
 #pragma unroll
       for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i), ta.x[c]);
       fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), SOFT);
-      fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, repl, scoef, sdd, sg, K, off);
+      fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, sab, scoef, sg, K, off);
 #pragma unroll
       for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i + 1), tb.x[c]);
       fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), SOFT);
     }
-    fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, repl, scoef, sdd, sg, K, off);
+    fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, sab, scoef, sg, K, off);
 #pragma unroll
     for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i), ta.x[c]);
     if (i + 1 < nsteps) {
-      fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, repl, scoef, sdd, sg, K, off);
+      fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, sab, scoef, sg, K, off);
 #pragma unroll
       for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i + 1), tb.x[c]);
     }
@@ -1353,14 +1503,14 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
     fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, SOFT);
-    fast_backward<C, VEC, SOFT, RIGHT>(t, tab, repl, scoef, sdd, sg, K, off);
+    fast_backward<C, VEC, SOFT, RIGHT>(t, tab, sab, scoef, sg, K, off);
 #pragma unroll
     for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + v, t.x[c]);
   }
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     FastTile<C, 1> t;
     fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, SOFT);
-    fast_backward<C, 1, SOFT, RIGHT>(t, tab, repl, scoef, sdd, sg, K, off);
+    fast_backward<C, 1, SOFT, RIGHT>(t, tab, sab, scoef, sg, K, off);
 #pragma unroll
     for (int c = 0; c < C; ++c) dr[c][v] = from_f32<T>(t.x[c][0]);
   }

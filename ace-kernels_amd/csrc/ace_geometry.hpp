@@ -45,9 +45,20 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 //   hard: u64 packed (count | label count | sum p), plus an i64 sum of the
 //         targets when they are per-channel values rather than labels
 //   soft: three i64 fixed-point sums W, P, G
-constexpr size_t hist_bytes_per_copy(int ck, bool soft, bool labels) {
-  return soft ? (size_t)ck * 24 : (size_t)ck * (labels ? 8 : 16);
+//   soft moments (softmax + labels): per half-bin (2K per channel) the packed
+//         word (count | label count | sum p), sum p^2 and sum p over the
+//         labelled voxels
+constexpr size_t hist_bytes_per_copy(int ck, bool soft, bool labels, bool moments = false) {
+  return moments ? (size_t)ck * 48 : (soft ? (size_t)ck * 24 : (size_t)ck * (labels ? 8 : 16));
 }
+
+// Final sums per batch index and replica: 3 x C'K (W, P, G per bin), or for
+// soft moments 5 x 2C'K (count, label count, sum p, sum p^2, sum p y per
+// half-bin).
+constexpr int fin_values(int ck, bool moments) { return moments ? 10 * ck : 3 * ck; }
+
+// Channel counts served by the fast (softmax + class-index labels) kernels.
+inline bool fast_channels(int64_t C) { return C == 2 || C == 3 || C == 4 || C == 16; }
 
 struct Geometry {
   Variant var;
@@ -62,6 +73,7 @@ struct Geometry {
   int reps;            // replicas of each batch index's final sums
   int copies;          // histogram copies (lane % copies)
   int lchunk;          // log2 of the copies one lane adds in the block sums
+  bool moments;        // soft binning through per-half-bin moments
   size_t tab_floats;   // padded bucket table (n + 2) + centre table (2K + 2)
   size_t lds_fwd;      // dynamic LDS of the forward kernel
   size_t lds_bwd;      // dynamic LDS of the backward kernel
@@ -71,10 +83,14 @@ struct Geometry {
 
 // Blocks per batch index: aim for ~8 blocks per CU on a 256-CU part while
 // keeping every block's tile a whole number of vector steps.
+// moments: the soft fast path (softmax + labels, fast_channels(C)) that bins
+// per-half-bin moments instead of per-voxel weights.
 inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
                               bool soft, bool include_background, bool labels,
-                              int steps_override = 0, int copies_override = 0) {
+                              int steps_override = 0, int copies_override = 0,
+                              bool moments = false) {
   Geometry g{};
+  g.moments = moments;
   g.var = variant_for(C);
   g.C = (int)C;
   g.off = (!include_background && C > 1) ? 1 : 0;
@@ -84,7 +100,7 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   g.B = B;
   g.N = N;
   // histogram copies: up to 32 (lane % 32), within the LDS budget
-  const size_t per_copy = hist_bytes_per_copy(g.ck, soft, labels);
+  const size_t per_copy = hist_bytes_per_copy(g.ck, soft, labels, moments);
   int copies = copies_override > 0 ? copies_override : 32;
   while (copies > 1 && per_copy * copies > (copies_override > 0 ? 160 * 1024 : kMaxHistLds))
     copies /= 2;
@@ -98,7 +114,7 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
     if (steps < 1) steps = 1;
     if (steps > 64) steps = 64;
   }
-  if (!soft) {
+  if (!soft || moments) {
     // every copy counts at most kMaxCopyCount voxels of a tile
     const int64_t max_steps = (int64_t)kMaxCopyCount * copies / step_vox;
     if (steps > max_steps) steps = (int)(max_steps > 0 ? max_steps : 1);
@@ -109,7 +125,7 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   // kThreads / copies lanes x steps x vec voxels)
   const int64_t copy_vox = (int64_t)(kThreads / copies) * steps * g.var.vec;
   int chunk = copies < 8 ? copies : 8;
-  while (chunk > 1 && !soft && chunk * copy_vox > kMaxCopyCount) chunk /= 2;
+  while (chunk > 1 && (!soft || moments) && chunk * copy_vox > kMaxCopyCount) chunk /= 2;
   int lchunk = 0;
   while ((1 << lchunk) < chunk) ++lchunk;
   g.lchunk = lchunk;
@@ -125,18 +141,21 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   const int n = soft ? 2 * K : K;
   g.tab_floats = align_up((size_t)(n + 2) + (soft ? (size_t)(2 * K + 2) : 0), 4);
   // the epilogue block reuses the histogram region: d, W, G (float) and an
-  // empty flag per bin of one batch index, then 4 floats of the loss sum
+  // empty flag per bin of one batch index, then 4 floats of the loss sum;
+  // moments also hold six float64 contributions per half-bin
   const size_t hist = align_up(per_copy * copies, 16);
-  const size_t epi = align_up((size_t)g.ck * 13, 16);
+  const size_t epi = align_up((size_t)g.ck * 16, 16) + (moments ? (size_t)g.ck * 96 : 0);
   const size_t region = hist > epi ? hist : epi;
   g.lds_fwd = g.tab_floats * 4 + region;
-  // backward: tables + coef (+ d) + g
-  g.lds_bwd = g.tab_floats * 4 + align_up((size_t)g.ck * (soft ? 2 : 1) + g.CL, 4) * 4;
+  // backward: tables + coef (+ d) + g (+ two coefficients per half-bin for
+  // soft moments)
+  g.lds_bwd = g.tab_floats * 4 +
+              align_up((size_t)g.ck * (soft ? 2 : 1) + ((g.CL + 1) & ~1) + (moments ? 4 * g.ck : 0), 4) * 4;
   // workspace: ticket counters (groups, batch indices, loss) and the final
   // sums; it must start zero and every call leaves it zero
   const int64_t counters = B * g.gpb + B + 1;
   g.off_fin = align_up((size_t)counters * kCtrStride * sizeof(int), 256);
-  const size_t fin_bytes = (size_t)B * g.reps * 3 * g.ck * sizeof(unsigned long long);
+  const size_t fin_bytes = (size_t)B * g.reps * fin_values(g.ck, moments) * sizeof(unsigned long long);
   g.ws_bytes = align_up(g.off_fin + fin_bytes, 256);
   return g;
 }
