@@ -219,6 +219,7 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   p.fin = reinterpret_cast<unsigned long long*>(ws + g.off_fin);
   p.reps = g.reps;
   p.lchunk = g.lchunk;
+  p.epi_all = g.epi_all ? 1 : 0;
   p.coef = coef;
   p.d = diff;
   p.jac = jac;

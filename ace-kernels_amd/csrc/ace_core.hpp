@@ -57,6 +57,7 @@ struct FwdParams {
   int B, C, off, K, act, tk, copies, vec_ok, ignore_empty, red;
   int reps;            // replicas of each batch index's final sums
   int lchunk;          // log2 of the copies one lane adds before unpacking
+  int epi_all;         // one block runs every batch index's epilogue and the loss
   float empty_w;
   const float* btab;   // bucket table (K or 2K upper boundaries)
   const float* rtab;   // soft centre table (2K + 2)
@@ -520,54 +521,67 @@ __device__ __forceinline__ void moment_terms(double n, double g, double s1, doub
   out[5] = (sg - cl * g) / S;
 }
 
+// Epilogue of batch indices [b0, b0 + nb) in one block.  Final sums -> W, P,
+// G per bin, d = P/W - G/W (kernels/epilogue.py:23-82); per class row: K_ne,
+// f, coef, jac (one wave per row).  It leaves its final sums zero.  With
+// `loss` (nb == B: the block holds every row) it also sums the per-class
+// errors into the loss, in row order.
 template <bool SOFT, bool MOM>
-__device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char* hist,
-                                               const float* repl, int CK, int CL, int b) {
+__device__ __forceinline__ void epilogue(const FwdParams& P, unsigned char* hist,
+                                         const float* repl, int CK, int CL, int b0, int nb,
+                                         bool loss) {
   const int tid = threadIdx.x;
   const int K = P.K;
   const int NV = fin_values(CK, MOM);
   const int reps = P.reps;
+  const EpiLayout L = epi_layout(CK, CL, nb, MOM);
+  const int NB = nb * CK;  // bins of this epilogue
   float* sd = reinterpret_cast<float*>(hist);
-  float* sw = sd + CK;
-  float* sg = sw + CK;
-  unsigned char* se = reinterpret_cast<unsigned char*>(sg + CK);
-  unsigned long long* fb = P.fin + (int64_t)b * reps * NV;
+  float* sw = sd + NB;
+  float* sg = sw + NB;
+  unsigned char* se = reinterpret_cast<unsigned char*>(sg + NB);
+  float* sf = reinterpret_cast<float*>(hist + L.sf);        // [nb * CL]
+  double* terms = reinterpret_cast<double*>(hist + L.terms);  // [nb * 2CK][6]
   const int64_t BCK = (int64_t)P.B * CK;
   const double dscale = 1.0 / 1073741824.0;
-  double* terms = reinterpret_cast<double*>(hist + 16 * (size_t)CK);  // [2CK][6]
   if constexpr (MOM) {
     // per half-bin: the five moments (every replica in flight at once), then
     // its six contributions
     const int H2 = 2 * CK;
-    for (int t = tid; t < H2; t += kThreads) {
+    for (int t = tid; t < nb * H2; t += kThreads) {
+      const int bb = t / H2;
+      const int th = t - bb * H2;
+      unsigned long long* fb = P.fin + (int64_t)(b0 + bb) * reps * NV;
       long long m[5] = {0, 0, 0, 0, 0};
 #pragma unroll
       for (int r = 0; r < kMaxReps; ++r) {
         if (r < reps) {
           unsigned long long* f = fb + (int64_t)r * NV;
 #pragma unroll
-          for (int v = 0; v < 5; ++v) m[v] += (long long)load_dev(&f[v * H2 + t]);
+          for (int v = 0; v < 5; ++v) m[v] += (long long)load_dev(&f[v * H2 + th]);
         }
       }
       for (int r = 0; r < reps; ++r) {
         unsigned long long* f = fb + (int64_t)r * NV;
 #pragma unroll
-        for (int v = 0; v < 5; ++v) store_dev(&f[v * H2 + t], 0ull);
+        for (int v = 0; v < 5; ++v) store_dev(&f[v * H2 + th], 0ull);
       }
-      const int hh = t % (2 * K);
+      const int hh = th % (2 * K);
       moment_terms((double)m[0], (double)m[1], (double)m[2] * dscale, (double)m[3] * dscale,
                    (double)m[4] * dscale, (double)repl[hh], (double)repl[hh + 2], terms + 6 * t);
     }
     __syncthreads();
   }
-  for (int t = tid; t < CK; t += kThreads) {
+  for (int i = tid; i < NB; i += kThreads) {
+    const int bb = i / CK;
+    const int t = i - bb * CK;
     double Wd, Pd, Gd;
     if constexpr (MOM) {
       // bin k of channel row cl: left share of half-bins l(h) = k, right share
       // of r(h) = k, h in [2k - 1, 2k + 2], in increasing h
       const int cl = t / K;
       const int k = t - cl * K;
-      const double* tb = terms + 6 * (size_t)(cl * 2 * K);
+      const double* tb = terms + 6 * ((size_t)bb * 2 * CK + (size_t)cl * 2 * K);
       Wd = Pd = Gd = 0.0;
       for (int hh = max(2 * k - 1, 0); hh <= min(2 * k + 2, 2 * K - 1); ++hh) {
         if ((max(hh - 1, 0) >> 1) == k) {
@@ -583,6 +597,7 @@ __device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char
       }
     } else {
       // every replica's three sums in flight at once (reps <= kMaxReps)
+      unsigned long long* fb = P.fin + (int64_t)(b0 + bb) * reps * NV;
       long long s0 = 0, s1 = 0, s2 = 0;
 #pragma unroll
       for (int r = 0; r < kMaxReps; ++r) {
@@ -603,7 +618,7 @@ __device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char
       Pd = (double)s1 * dscale;
       Gd = (double)s2 * dscale;
     }
-    const int64_t o = (int64_t)b * CK + t;
+    const int64_t o = (int64_t)(b0 + bb) * CK + t;
     if (P.stats) {
       P.stats[o] = Wd;
       P.stats[BCK + o] = Pd;
@@ -614,18 +629,20 @@ __device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char
     const float Gf = (float)Gd;
     const bool empty = SOFT ? !(Wf >= P.empty_w) : (Wf == 0.0f);
     const float dd = empty ? 0.0f : (Pf / Wf - Gf / Wf);
-    sd[t] = dd;
-    sw[t] = Wf;
-    sg[t] = Gf;
-    se[t] = empty ? 1 : 0;
+    sd[i] = dd;
+    sw[i] = Wf;
+    sg[i] = Gf;
+    se[i] = empty ? 1 : 0;
     P.d[o] = dd;
   }
   __syncthreads();
   // one wave per class row
   const int lane = tid & 63;
   const int rows = P.B * CL;
-  for (int cl = tid >> 6; cl < CL; cl += kThreads / 64) {
-    const int base = cl * K;
+  for (int row = tid >> 6; row < nb * CL; row += kThreads / 64) {
+    const int base = row * K;  // == bb * CK + cl * K
+    const int bb = row / CL;
+    const int cl = row - bb * CL;
     int kne = 0;
     float err = 0.0f, gsum = 0.0f;
     for (int k = lane; k < K; k += 64) {
@@ -641,10 +658,11 @@ __device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char
     const float fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
     const float present = gsum > 0.0f ? 1.0f : 0.0f;
     const float kf = (float)(kne > 0 ? kne : 1);
+    const int64_t ob = (int64_t)(b0 + bb) * CK + cl * K;
     for (int k = lane; k < K; k += 64) {
       const float dd = sd[base + k];
       const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
-      P.coef[(int64_t)b * CK + base + k] = se[base + k] ? 0.0f : sgn / (kf * sw[base + k]);
+      P.coef[ob + k] = se[base + k] ? 0.0f : sgn / (kf * sw[base + k]);
     }
     if (lane == 0) {
       const float w = P.clsw ? P.clsw[cl] : 1.0f;
@@ -652,8 +670,23 @@ __device__ __forceinline__ void batch_epilogue(const FwdParams& P, unsigned char
       fw = fw * w;
       float jac = P.ignore_empty ? present * w : w;
       if (P.red == kRedMean) jac = jac / (float)rows;
-      store_dev(&P.f[b * CL + cl], fw);
-      P.jac[b * CL + cl] = jac;
+      const int gi = (b0 + bb) * CL + cl;
+      if (loss) {
+        P.f[gi] = fw;
+        sf[row] = fw;
+      } else {
+        store_dev(&P.f[gi], fw);
+      }
+      P.jac[gi] = jac;
+    }
+  }
+  if (loss && P.red != kRedNone) {
+    __syncthreads();
+    if (tid == 0) {
+      float total = 0.0f;
+      for (int r = 0; r < rows; ++r) total += sf[r];
+      if (P.red == kRedMean) total = total / (float)rows;
+      P.loss[0] = total;
     }
   }
 }
@@ -794,15 +827,22 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
     int* gc = counter(P, (int64_t)b * P.gpb + g);
     if (ticket(gc) == (int)gsize - 1) {
       __hip_atomic_store(gc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      int* bc = counter(P, (int64_t)P.B * P.gpb + b);
-      last = ticket(bc) == (int)P.gpb - 1;
+      // the last group of batch b -- or, with one epilogue block for all
+      // batch indices, the last group of all
+      int* bc = counter(P, (int64_t)P.B * P.gpb + (P.epi_all ? 0 : b));
+      const int arrivals = P.epi_all ? (int)(P.B * P.gpb) : (int)P.gpb;
+      last = ticket(bc) == arrivals - 1;
       if (last) __hip_atomic_store(bc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     s_last = last;
   }
   __syncthreads();
   if (!s_last) return;
-  batch_epilogue<SOFT, MOM>(P, hist, repl, CK, CL, b);
+  if (P.epi_all) {
+    epilogue<SOFT, MOM>(P, hist, repl, CK, CL, 0, P.B, true);
+    return;
+  }
+  epilogue<SOFT, MOM>(P, hist, repl, CK, CL, b, 1, false);
   if (P.red == kRedNone) return;
 
   // ---- loss: the last batch epilogue sums the B x C' per-class errors

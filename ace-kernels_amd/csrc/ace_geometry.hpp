@@ -57,6 +57,21 @@ constexpr size_t hist_bytes_per_copy(int ck, bool soft, bool labels, bool moment
 // half-bin).
 constexpr int fin_values(int ck, bool moments) { return moments ? 10 * ck : 3 * ck; }
 
+// LDS layout of an epilogue over nb batch indices (byte offsets from the
+// histogram region): d, W, G (float) and an empty flag per bin, the per-class
+// errors, and for soft moments six float64 contributions per half-bin.
+struct EpiLayout {
+  size_t sf, terms, bytes;
+};
+constexpr size_t align16(size_t v) { return (v + 15) / 16 * 16; }
+constexpr EpiLayout epi_layout(int ck, int cl, int nb, bool moments) {
+  return EpiLayout{align16((size_t)13 * ck * nb),
+                   align16(align16((size_t)13 * ck * nb) + (size_t)4 * cl * nb),
+                   align16(align16((size_t)13 * ck * nb) + (size_t)4 * cl * nb) +
+                       (moments ? (size_t)96 * ck * nb : 0)};
+}
+constexpr int kMaxEpiRows = 16;  // C' up to which a single batch index's epilogue sums the loss
+
 // Channel counts served by the fast (softmax + class-index labels) kernels.
 inline bool fast_channels(int64_t C) { return C == 2 || C == 3 || C == 4 || C == 16; }
 
@@ -74,6 +89,7 @@ struct Geometry {
   int copies;          // histogram copies (lane % copies)
   int lchunk;          // log2 of the copies one lane adds in the block sums
   bool moments;        // soft binning through per-half-bin moments
+  bool epi_all;        // one block runs the epilogue of every batch index
   size_t tab_floats;   // padded bucket table (n + 2) + centre table (2K + 2)
   size_t lds_fwd;      // dynamic LDS of the forward kernel
   size_t lds_bwd;      // dynamic LDS of the backward kernel
@@ -140,11 +156,13 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   g.reps = (int)(reps > kMaxReps ? kMaxReps : reps);
   const int n = soft ? 2 * K : K;
   g.tab_floats = align_up((size_t)(n + 2) + (soft ? (size_t)(2 * K + 2) : 0), 4);
-  // the epilogue block reuses the histogram region: d, W, G (float) and an
-  // empty flag per bin of one batch index, then 4 floats of the loss sum;
-  // moments also hold six float64 contributions per half-bin
+  // the epilogue block reuses the histogram region (epi_layout).  With one
+  // batch index its epilogue block also sums the loss (no loss ticket); with
+  // more, batch epilogues run in parallel blocks (one block doing several
+  // measured slower on MI355X), then the last one sums the loss.
   const size_t hist = align_up(per_copy * copies, 16);
-  const size_t epi = align_up((size_t)g.ck * 16, 16) + (moments ? (size_t)g.ck * 96 : 0);
+  g.epi_all = B == 1 && g.CL <= kMaxEpiRows;
+  const size_t epi = epi_layout(g.ck, g.CL, 1, moments).bytes;
   const size_t region = hist > epi ? hist : epi;
   g.lds_fwd = g.tab_floats * 4 + region;
   // backward: tables + coef (+ d) + g (+ two coefficients per half-bin for
