@@ -23,6 +23,7 @@ float64, ``v6_triton.py:226-227``; this package has no non-HIP path).
 
 from __future__ import annotations
 
+from functools import lru_cache
 from typing import Any, Optional, Tuple
 
 import torch
@@ -204,3 +205,101 @@ register(
     description="MI355X HIP kernels: fused softmax/binning/histogram forward, one-pass backward",
     devices=frozenset({"cuda"}),
 )(hip_ace)
+
+
+# ---------------------------------------------------------------- custom ops
+# The same kernels as ``torch.library`` custom ops with fake (meta) kernels
+# and an autograd formula, so that ``torch.compile(fullgraph=True)`` of a
+# network plus this loss traces through it without graph breaks -- the
+# packaging of the reference's ``v6_forward`` / ``v6_backward``
+# (``src/ace_kernels/impls/v6_triton.py:141-216``).  The config travels as its
+# JSON text, a compile-time constant.
+
+Outputs = Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]
+
+
+@lru_cache(maxsize=64)
+def _config(config_json: str) -> ACEConfig:
+    return ACEConfig.model_validate_json(config_json)
+
+
+def _dump(config: ACEConfig) -> str:
+    return config.model_dump_json()
+
+
+# constant for torch.compile (pydantic models are not traceable): a compiled
+# function must not swap configs between calls
+config_arg = torch.compiler.assume_constant_result(_dump)
+
+
+@torch.library.custom_op("ace_kernels::hip_forward", mutates_args=())
+def hip_forward_op(input: torch.Tensor, target: torch.Tensor, config_json: str) -> Outputs:
+    """mL1-ACE forward: (loss, coef, d, jac) from one ``ace_forward`` launch."""
+    config = _config(config_json)
+    loss, coef, d, jac, _, _ = hip_forward(make_plan(input, target, config), config)
+    # a custom op may not return a view of an internal buffer: copy the "none" view
+    return (loss.clone() if loss.dim() else loss), coef, d, jac
+
+
+@hip_forward_op.register_fake
+def _(input: torch.Tensor, target: torch.Tensor, config_json: str) -> Outputs:
+    config = _config(config_json)
+    b, c = input.shape[:2]
+    cl = c - (1 if (not config.include_background and c > 1) else 0)
+    per_bin = input.new_empty((b, cl, config.num_bins), dtype=torch.float32)
+    loss_shape = (b, cl, *([1] * (input.dim() - 2))) if config.reduction == "none" else ()
+    loss = input.new_empty(loss_shape, dtype=torch.float32)
+    jac = input.new_empty((b, cl), dtype=torch.float32)
+    return loss, per_bin, torch.empty_like(per_bin), jac
+
+
+@torch.library.custom_op("ace_kernels::hip_backward", mutates_args=())
+def hip_backward_op(input: torch.Tensor, target: torch.Tensor, coef: torch.Tensor,
+                    d: torch.Tensor, jac: torch.Tensor, grad_output: torch.Tensor,
+                    config_json: str) -> torch.Tensor:
+    """d loss / d input from one ``ace_backward`` launch."""
+    return hip_backward(make_plan(input, target, _config(config_json)), coef, d, jac, grad_output)
+
+
+@hip_backward_op.register_fake
+def _(input: torch.Tensor, target: torch.Tensor, coef: torch.Tensor, d: torch.Tensor,
+      jac: torch.Tensor, grad_output: torch.Tensor, config_json: str) -> torch.Tensor:
+    return torch.empty_like(input)
+
+
+def _setup_context(ctx: Any, inputs: Tuple[Any, ...], output: Outputs) -> None:
+    input, target, config_json = inputs
+    _, coef, d, jac = output
+    ctx.config_json = config_json
+    ctx.set_materialize_grads(False)  # coef / d / jac get no gradient: no zero fills
+    ctx.save_for_backward(input, target, coef, d, jac)
+
+
+def _op_backward(ctx: Any, grad_loss: torch.Tensor, *_unused: torch.Tensor):
+    input, target, coef, d, jac = ctx.saved_tensors
+    dx = hip_backward_op(input, target, coef, d, jac, grad_loss, ctx.config_json)
+    return dx, None, None
+
+
+hip_forward_op.register_autograd(_op_backward, setup_context=_setup_context)
+
+
+def hip_ace_op(input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> torch.Tensor:
+    """Registry entry over the custom ops (compile-friendly)."""
+    loss: torch.Tensor = hip_forward_op(input, target, config_arg(config))[0]
+    return loss
+
+
+def hip_ace_op_json(input: torch.Tensor, target: torch.Tensor, config_json: str) -> torch.Tensor:
+    """The custom ops with the config already as JSON text: what the drop-in
+    modules call under ``torch.compile`` (a string attribute is a trace-time
+    constant; this torch version cannot fold the pydantic config itself)."""
+    loss: torch.Tensor = hip_forward_op(input, target, config_json)[0]
+    return loss
+
+
+register(
+    "hip_mi355x_op",
+    description="hip_mi355x as torch.library custom ops (torch.compile without graph breaks)",
+    devices=frozenset({"cuda"}),
+)(hip_ace_op)
