@@ -1139,38 +1139,16 @@ struct FastTile {
   long long lab[VEC];  // raw int64 labels, converted when used
 };
 
-// 16-byte load, non-temporal when NT (the forward reads its inputs once: a
-// streaming load keeps them from displacing other lines; measured ~1 us
-// faster on the forward at 128^3, neutral on the backward)
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-template <bool NT>
-__device__ __forceinline__ u32x4_t load16(const void* p) {
-  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-  return *reinterpret_cast<const u32x4_t*>(p);
-}
-
-template <typename T, int C, int VEC, bool NT = false>
+template <typename T, int C, int VEC>
 __device__ __forceinline__ void fast_load(FastTile<C, VEC>& t, const T* const (&xr)[C],
                                           const long long* lr, uint32_t v, bool with_labels) {
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
-    if constexpr (NT && sizeof(T) * VEC == 16) {
-      const u32x4_t raw = load16<true>(xr[c] + v);
-      T vals[VEC];
-      __builtin_memcpy(vals, &raw, 16);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) t.x[c][j] = to_f32<T>(vals[j]);
-    } else {
-      load_vec<T, VEC>(xr[c] + v, t.x[c]);
-    }
-  }
+  for (int c = 0; c < C; ++c) load_vec<T, VEC>(xr[c] + v, t.x[c]);
   if (with_labels) {
     if constexpr (VEC % 2 == 0) {
 #pragma unroll
       for (int j = 0; j < VEC; j += 2) {
-        const u32x4_t raw = load16<NT>(lr + v + j);
-        longlong2 q;
-        __builtin_memcpy(&q, &raw, 16);
+        const longlong2 q = *reinterpret_cast<const longlong2*>(lr + v + j);
         t.lab[j] = q.x;
         t.lab[j + 1] = q.y;
       }
@@ -1349,8 +1327,8 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
 #pragma unroll
     for (int c = 0; c < C; ++c) px[c] = pipe ? xr[c] : reinterpret_cast<const T*>(g_dummy_src);
     const long long* pl = pipe ? lr_ : reinterpret_cast<const long long*>(g_dummy_src);
-    fast_load<T, C, VEC, true>(ta, px, pl, pipe ? at(0) : 0u, true);
-    fast_load<T, C, VEC, true>(tb, px, pl, pipe ? at(1) : 0u, true);
+    fast_load<T, C, VEC>(ta, px, pl, pipe ? at(0) : 0u, true);
+    fast_load<T, C, VEC>(tb, px, pl, pipe ? at(1) : 0u, true);
   }
   treg.store(tabs, P.btab, P.rtab, n, nrepl);
   {
@@ -1372,9 +1350,9 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
     int i = 0;
     for (; i + 2 < nsteps; i += 2) {
       fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, skip0, lsh, hb, words);
-      fast_load<T, C, VEC, true>(ta, xr, lr_, at(i + 2), true);
+      fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), true);
       fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, skip0, lsh, hb, words);
-      fast_load<T, C, VEC, true>(tb, xr, lr_, at(i + 3), true);
+      fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), true);
     }
     fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, skip0, lsh, hb, words);
     if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, skip0, lsh, hb, words);
@@ -1382,12 +1360,12 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   // remaining full vectors (not every thread has one), then single voxels
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
-    fast_load<T, C, VEC, true>(t, xr, lr_, (uint32_t)v, true);
+    fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, true);
     fast_accumulate<C, VEC, SOFT, RIGHT>(t, tab, repl, K, skip0, lsh, hb, words);
   }
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     FastTile<C, 1> t;
-    fast_load<T, C, 1, true>(t, xr, lr_, (uint32_t)v, true);
+    fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, true);
     fast_accumulate<C, 1, SOFT, RIGHT>(t, tab, repl, K, skip0, lsh, hb, words);
   }
   __syncthreads();
