@@ -691,114 +691,135 @@ __device__ __forceinline__ void epilogue(const FwdParams& P, unsigned char* hist
   }
 }
 
-// Sums the R histogram copies of every bin and adds the block's 3 x CK sums
-// into `fin` with integer atomics.  Q = R / chunk neighbouring lanes share a
-// bin: each adds `chunk` copies (hard: packed words, added before decoding --
-// the geometry keeps chunk x per-copy counts within the 11-bit fields), then
-// the Q lanes combine with shuffles and the first one issues the atomics, so
-// one wave request covers 64 / Q consecutive bins.  The copy index is skewed
-// by the bin so that the lanes of a wave read distinct bank pairs.
-// Moments variant: 5 values per half-bin (count, labelled count, sum p,
-// sum p^2, labelled sum p; the counts unscaled), fin layout [5][2CK].
-__device__ __forceinline__ void block_moments(const FwdParams& P, const Hist& H, int CK,
-                                              unsigned long long* fin) {
-  const int tid = threadIdx.x;
-  const int R = P.copies;
-  const int chunk = 1 << P.lchunk;
-  const int lq = __builtin_ctz((unsigned)R) - P.lchunk;
-  const int Q = 1 << lq;
-  const int H2 = 2 * CK;
-  const int total = H2 << lq;
-  for (int base = 0; base < total; base += kThreads) {
-    const int i = base + tid;
-    const int t = i >> lq;
-    const int part = i & (Q - 1);
-    long long m[5] = {0, 0, 0, 0, 0};
-    if (t < H2) {
-      const int w0 = t * R + part * chunk;
-      unsigned long long a = 0, q2 = 0, qg = 0;
+// Block sums: one lane per bin (half-bin for moments) loads the R copies of
+// that bin, adds them -- packed words `chunk` at a time, decoded after each
+// chunk (the geometry keeps chunk x per-copy counts within the 11-bit fields)
+// -- and issues the atomics into `fin`, so one wave request covers 64
+// consecutive final sums and no lanes combine.  R is a template argument so
+// that the loads are unconditional and issue back to back; the copy index is
+// skewed by the bin so that the lanes of a wave read distinct bank pairs.
+
+// Adds the decoded fields of a sum of packed words (count | label count |
+// sum p): counts unscaled, sum p signed (probabilities outside [0, 1] without
+// an activation) -- the upper fields are rounded so that it decodes in
+// [-2^41, 2^41).
+__device__ __forceinline__ void decode_packed(unsigned long long a, long long& n, long long& g,
+                                              long long& sp) {
+  const unsigned long long hi = (a + (1ull << (kShiftG - 1))) >> kShiftG;
+  n += (long long)(hi >> (kShiftN - kShiftG));
+  g += (long long)(hi & ((1ull << (kShiftN - kShiftG)) - 1));
+  sp += (long long)(a - (hi << kShiftG));
+}
+
+// Copies one lane loads before adding them: bounds the registers the block
+// sums hold (the kernel's register count is that of its widest phase).
+constexpr int kSumBatch = 8;
+
+// Sum of the R packed copies starting at w0 (skew s), decoded every `chunk`.
+template <int R, int BATCH = kSumBatch>
+__device__ __forceinline__ void sum_packed(const unsigned long long* a, int w0, int s, int chunk,
+                                           long long& n, long long& g, long long& sp) {
+  constexpr int NB = R < BATCH ? R : BATCH;
+  unsigned long long acc = 0;
+#pragma unroll 1
+  for (int r0 = 0; r0 < R; r0 += NB) {
+    unsigned long long v[NB];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j < chunk) {
-          const int w = w0 + ((j + t) & (chunk - 1));
-          a += H.a[w];
-          q2 += H.m2[w];
-          qg += H.mg[w];
-        }
+    for (int j = 0; j < NB; ++j) v[j] = a[w0 + ((r0 + j + s) & (R - 1))];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      acc += v[j];
+      if (((r0 + j + 1) & (chunk - 1)) == 0) {
+        decode_packed(acc, n, g, sp);
+        acc = 0;
       }
-      const unsigned long long hi = (a + (1ull << (kShiftG - 1))) >> kShiftG;
-      m[0] = (long long)(hi >> (kShiftN - kShiftG));
-      m[1] = (long long)(hi & ((1ull << (kShiftN - kShiftG)) - 1));
-      m[2] = (long long)(a - (hi << kShiftG));
-      m[3] = (long long)q2;
-      m[4] = (long long)qg;
-    }
-#pragma unroll
-    for (int v = 0; v < 5; ++v)
-      for (int o = 1; o < Q; o <<= 1) m[v] += __shfl_xor(m[v], o, 64);
-    if (t < H2 && part == 0) {
-#pragma unroll
-      for (int v = 0; v < 5; ++v)
-        if (m[v]) atomicAdd(&fin[v * H2 + t], (unsigned long long)m[v]);
     }
   }
+}
+
+template <int R, int BATCH = kSumBatch, typename T>
+__device__ __forceinline__ long long sum_copies(const T* a, int w0, int s) {
+  constexpr int NB = R < BATCH ? R : BATCH;
+  long long acc = 0;
+#pragma unroll 1
+  for (int r0 = 0; r0 < R; r0 += NB) {
+    T v[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) v[j] = a[w0 + ((r0 + j + s) & (R - 1))];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc += (long long)v[j];
+  }
+  return acc;
+}
+
+// Moments variant: 5 values per half-bin (count, labelled count, sum p,
+// sum p^2, labelled sum p; counts unscaled), fin layout [5][2CK].
+template <int R>
+__device__ __forceinline__ void block_moments_r(const FwdParams& P, const Hist& H, int CK,
+                                                unsigned long long* fin) {
+  const int chunk = 1 << P.lchunk;
+  const int H2 = 2 * CK;
+  for (int t = threadIdx.x; t < H2; t += kThreads) {
+    long long m[5] = {0, 0, 0, 0, 0};
+    // three arrays: half batches keep the registers of the main loop's
+    sum_packed<R, kSumBatch / 2>(H.a, t * R, t, chunk, m[0], m[1], m[2]);
+    m[3] = sum_copies<R, kSumBatch / 2>(H.m2, t * R, t);
+    m[4] = sum_copies<R, kSumBatch / 2>(H.mg, t * R, t);
+#pragma unroll
+    for (int v = 0; v < 5; ++v)
+      if (m[v]) atomicAdd(&fin[v * H2 + t], (unsigned long long)m[v]);
+  }
+}
+
+template <int R, bool SOFT>
+__device__ __forceinline__ void block_sums_r(const FwdParams& P, const Hist& H, int CK, bool labels,
+                                             unsigned long long* fin) {
+  const int chunk = 1 << P.lchunk;
+  for (int t = threadIdx.x; t < CK; t += kThreads) {
+    long long s0, s1 = 0, s2;
+    if constexpr (!SOFT) {
+      long long n = 0, g = 0;
+      sum_packed<R>(H.a, t * R, t, chunk, n, g, s1);
+      s0 = n << kFrac;
+      s2 = labels ? (g << kFrac) : sum_copies<R>(H.g1, t * R, t);
+    } else {
+      s0 = sum_copies<R>(H.w, t * R, t);
+      s1 = sum_copies<R>(H.p, t * R, t);
+      s2 = sum_copies<R>(H.g, t * R, t);
+    }
+    if (s0) atomicAdd(&fin[t], (unsigned long long)s0);
+    if (s1) atomicAdd(&fin[CK + t], (unsigned long long)s1);
+    if (s2) atomicAdd(&fin[2 * CK + t], (unsigned long long)s2);
+  }
+}
+
+// Copies per block are a power of two <= 64.
+#define ACE_SWITCH_COPIES(R_, CALL) \
+  switch (R_) {                     \
+    case 1: CALL(1); break;         \
+    case 2: CALL(2); break;         \
+    case 4: CALL(4); break;         \
+    case 8: CALL(8); break;         \
+    case 16: CALL(16); break;       \
+    case 32: CALL(32); break;       \
+    default: CALL(64); break;       \
+  }
+
+__device__ __forceinline__ void block_moments(const FwdParams& P, const Hist& H, int CK,
+                                              unsigned long long* fin) {
+#define ACE_MOM(R) block_moments_r<R>(P, H, CK, fin)
+  ACE_SWITCH_COPIES(P.copies, ACE_MOM)
+#undef ACE_MOM
 }
 
 template <bool SOFT>
 __device__ __forceinline__ void block_sums(const FwdParams& P, const Hist& H, int CK, bool labels,
                                            unsigned long long* fin) {
-  const int tid = threadIdx.x;
-  const int R = P.copies;
-  const int chunk = 1 << P.lchunk;
-  const int lq = __builtin_ctz((unsigned)R) - P.lchunk;
-  const int Q = 1 << lq;
-  const int total = CK << lq;
-  for (int base = 0; base < total; base += kThreads) {
-    const int i = base + tid;
-    const int t = i >> lq;
-    const int part = i & (Q - 1);
-    long long s0 = 0, s1 = 0, s2 = 0;
-    if (t < CK) {
-      const int w0 = t * R + part * chunk;
-      if constexpr (!SOFT) {
-        unsigned long long a = 0;
-        long long gy = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (j < chunk) {
-            const int w = w0 + ((j + t) & (chunk - 1));
-            a += H.a[w];
-            if (!labels) gy += H.g1[w];
-          }
-        }
-        // the sum-p field is signed (probabilities outside [0, 1] without an
-        // activation): round the upper fields so that it decodes in
-        // [-2^41, 2^41)
-        const unsigned long long hi = (a + (1ull << (kShiftG - 1))) >> kShiftG;
-        s0 = (long long)((hi >> (kShiftN - kShiftG)) << kFrac);
-        s1 = (long long)(a - (hi << kShiftG));
-        s2 = labels ? (long long)((hi & ((1ull << (kShiftN - kShiftG)) - 1)) << kFrac) : gy;
-      } else {
-        for (int j = 0; j < chunk; ++j) {
-          const int w = w0 + ((j + t) & (chunk - 1));
-          s0 += H.w[w];
-          s1 += H.p[w];
-          s2 += H.g[w];
-        }
-      }
-    }
-    for (int o = 1; o < Q; o <<= 1) {
-      s0 += __shfl_xor(s0, o, 64);
-      s1 += __shfl_xor(s1, o, 64);
-      s2 += __shfl_xor(s2, o, 64);
-    }
-    if (t < CK && part == 0) {
-      if (s0) atomicAdd(&fin[t], (unsigned long long)s0);
-      if (s1) atomicAdd(&fin[CK + t], (unsigned long long)s1);
-      if (s2) atomicAdd(&fin[2 * CK + t], (unsigned long long)s2);
-    }
-  }
+#define ACE_SUMS(R) block_sums_r<R, SOFT>(P, H, CK, labels, fin)
+  ACE_SWITCH_COPIES(P.copies, ACE_SUMS)
+#undef ACE_SUMS
 }
+#undef ACE_SWITCH_COPIES
 
 // ---- end of a forward block.  Adds the block's sums into replica
 // (tile % reps) of batch b's final sums (fixed point: exact and

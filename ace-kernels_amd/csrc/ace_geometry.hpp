@@ -136,11 +136,11 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
     if (steps > max_steps) steps = (int)(max_steps > 0 ? max_steps : 1);
   }
   g.steps = steps;
-  // block sums: a lane adds up to 8 copies; hard packed words only as many as
-  // keep the count fields within kMaxCopyCount (a copy counts at most
-  // kThreads / copies lanes x steps x vec voxels)
+  // block sums: a lane adds the packed words of as many copies as keep the
+  // count fields within kMaxCopyCount before decoding them (a copy counts at
+  // most kThreads / copies lanes x steps x vec voxels)
   const int64_t copy_vox = (int64_t)(kThreads / copies) * steps * g.var.vec;
-  int chunk = copies < 8 ? copies : 8;
+  int chunk = copies;
   while (chunk > 1 && (!soft || moments) && chunk * copy_vox > kMaxCopyCount) chunk /= 2;
   int lchunk = 0;
   while ((1 << lchunk) < chunk) ++lchunk;
