@@ -216,6 +216,7 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   p.clsw = class_weight;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   p.ctr = reinterpret_cast<int*>(ws);
+  p.part = reinterpret_cast<unsigned long long*>(ws + g.off_part);
   p.fin = reinterpret_cast<unsigned long long*>(ws + g.off_fin);
   p.reps = g.reps;
   p.lchunk = g.lchunk;

@@ -23,24 +23,56 @@ namespace ace {
 // because the table is sorted.  `tab` is padded: tab[0] = -inf,
 // tab[1 + j] = table[j], tab[n + 1] = +inf, so both neighbours of the first
 // guess are read together.
-// CLAMP = true clamps p * n to [0, n] and the result to [0, n - 1]: p > 1 + eps32
-// and NaN are outside the reference's domain (its scatter raises for them), and
-// the clamp keeps every histogram index in range.
-// CLAMP = false is for probabilities known to lie in [0, 1] (softmax output):
-// p * n is then in [0, n] and the result in [0, n - 1] (the last table entry,
-// 1 + eps, exceeds p); a NaN p is mapped to g = 0 by fmaxf and fails both
-// checks, so it lands in bin 0.
-template <bool RIGHT, bool CLAMP = true>
+// p * n is clamped to [0, n] and the result to [0, n - 1]: p > 1 + eps32 and
+// NaN are outside the reference's domain (its scatter raises for them), and
+// the clamp keeps every histogram index in range.  Probabilities known to lie
+// in [0, 1] (softmax output) take bucket_unit below, with one check.
+template <bool RIGHT>
 ACE_HD int bucket(float p, float nf, int n, const float* tab) {
-  const float t = CLAMP ? fminf(fmaxf(p * nf, 0.0f), nf) : fmaxf(p * nf, 0.0f);  // fmaxf(NaN, 0) = 0
+  const float t = fminf(fmaxf(p * nf, 0.0f), nf);  // fmaxf(NaN, 0) = 0
   const int g = (int)t;                            // t >= 0: truncation is floor
   const float lo = tab[g];                         // table[g - 1]
   const float hi = tab[g + 1];                     // table[g]
   const bool up = RIGHT ? (hi <= p) : (hi < p);
   const bool down = RIGHT ? (lo > p) : (lo >= p);
   const int g2 = g + (up ? 1 : 0) - (down ? 1 : 0);
-  if (!CLAMP) return g2;
   return g2 < 0 ? 0 : (g2 > n - 1 ? n - 1 : g2);
+}
+
+// a / b correctly rounded from y = RN(1 / b) (Markstein): q = RN(a y) is
+// within an ulp, the residual a - b q is exact, and RN(q + r y) is the IEEE
+// quotient while a and a / b stay >= 2^-100 (the residual then does not
+// underflow).  Three instructions.
+ACE_HD float div_rn(float a, float b, float y) {
+  const float q = a * y;
+  const float r = fmaf(-b, q, a);
+  return fmaf(r, y, q);
+}
+
+// Bin of a probability p in [0, 1] (or NaN -> 0) with a single correction:
+// the first guess g = trunc(p * n - 1/4) is the bin k or k - 1, never more
+// or less, so one comparison with the upper edge of bin g fixes it.  With
+// the float32 edges e_j = linspace(0, 1 + eps, n + 1)[j + 1] = (j + 1) / n
+// times (1 + d_j), |d_j| < 8 * 2^-24 (eps and torch's float32 rounding), and
+// the fused p * n - 1/4 rounded once:
+//   p <= e_k      gives p * n - 1/4 <= k + 3/4 + (k + 1) * 8 * 2^-24 < k + 1
+//                 for n < 2^19, so g <= k;
+//   p >  e_{k-1}  gives p * n - 1/4 > k - 1/4 - k * 8 * 2^-24 > k - 1, so
+//                 g >= k - 1 (and g = 0 when k = 0).
+// g <= n - 1 for p <= 1, and e_{n-1} = 1 + eps > 1, so no clamp is needed.
+// tab is the padded table (tab[j + 1] = e_j).  NaN bins to 0: the device
+// conversion is v_cvt_i32_f32, which maps NaN to 0.
+template <bool RIGHT>
+ACE_HD int bucket_unit(float p, float nf, const float* tab) {
+  const float t = fmaf(p, nf, -0.25f);
+#if defined(__HIP_DEVICE_COMPILE__)
+  int g;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(g) : "v"(t));
+#else
+  const int g = t == t ? (int)t : 0;
+#endif
+  const float e = tab[g + 1];
+  return g + ((RIGHT ? (e <= p) : (e < p)) ? 1 : 0);
 }
 
 }  // namespace ace

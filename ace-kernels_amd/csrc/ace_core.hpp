@@ -65,6 +65,7 @@ struct FwdParams {
   unsigned long long* fin;  // [B][reps][3][CK] zeroed final sums (reset by the epilogues)
   int* ctr;            // zeroed ticket counters, kCtrStride ints apart:
                        // [B * gpb] groups, [B] batch indices, [1] loss
+  unsigned long long* part;  // [B] zeroed loss partial words: 1 << 32 | float bits
   float* coef;
   float* d;
   float* jac;
@@ -173,21 +174,27 @@ __device__ __forceinline__ void load_row(const T* __restrict__ p, float (&out)[V
 // Correctly rounded a / b with the reciprocal y = rcp_rn(b) shared by every
 // numerator over b: y is v_rcp_f32 refined by one Newton step, which equals the
 // IEEE quotient 1 / b for every float b in [2^-20, 2^20) (checked exhaustively
-// on MI355X); given y = RN(1 / b), two residual corrections of a * y give the
-// IEEE quotient (Markstein's theorem), checked against '/' for 2e10 (a, b)
-// pairs.  Used where b is a softmax sum in [1, C] or a soft-bin span in
-// [2^-20, 2^14]; bit-identical to '/', at a quarter of its instructions.
+// on MI355X).  Given y = RN(1 / b) and q = RN(a y) within an ulp of a / b, the
+// residual r = a - b q is exact and RN(q + r y) is the IEEE quotient
+// (Markstein's theorem) as long as r does not underflow: checked against '/'
+// for every float b in [2^-20, 2^14) with a of every exponent, no mismatch
+// where a and a / b are >= 2^-100.  Below that (softmax terms e^-69 and
+// smaller) the quotient may be an ulp off, far below any bin edge or
+// tolerance.  Used where b is a softmax sum in [1, C] or a soft-bin span in
+// [2^-20, 2^14]: three instructions per quotient.
 __device__ __forceinline__ float rcp_rn(float b) {
   const float y = __builtin_amdgcn_rcpf(b);
   const float e = fmaf(-b, y, 1.0f);
   return fmaf(e, y, y);
 }
-__device__ __forceinline__ float div_rn(float a, float b, float y) {
-  float q = a * y;
-  float r = fmaf(-b, q, a);
-  q = fmaf(r, y, q);
-  r = fmaf(-b, q, a);
-  return fmaf(r, y, q);
+// div_rn(a, b, y): ace_bins.hpp (shared with the CPU test harness).
+
+// p in [0, 1] (or NaN) in 30-bit fixed point, truncated: v_cvt_u32_f32 rounds
+// toward zero and maps NaN to 0.  At most 2^-30 below p.
+__device__ __forceinline__ uint32_t fixq(float p) {
+  uint32_t q;
+  asm("v_cvt_u32_f32 %0, %1" : "=v"(q) : "v"(p * 1073741824.0f));
+  return q;
 }
 
 // ------------------------------------------------------------ activation
@@ -250,11 +257,11 @@ struct SoftW {
 // half boundaries; bins l = max(h-1,0)/2, r = min(h+1,2K-1)/2; distances to
 // the replicated centres (sentinels +-1e4); lw = rd/S, rw = ld/S and 1/S, all
 // IEEE quotients (one shared reciprocal of S).
-template <bool RIGHT, bool CLAMP = true>
+template <bool RIGHT>
 __device__ __forceinline__ SoftW soft_assign(float p, int K, float n2f, const float* htab,
                                              const float* repl) {
   const int n2 = 2 * K;
-  const int h = bucket<RIGHT, CLAMP>(p, n2f, n2, htab);
+  const int h = bucket<RIGHT>(p, n2f, n2, htab);
   SoftW w;
   w.l = max(h - 1, 0) >> 1;
   w.r = min(h + 1, n2 - 1) >> 1;
@@ -321,6 +328,9 @@ __device__ __forceinline__ void wait_own_writes() {
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
+// Polls of another block's loss partial word before the loss gives up (NaN):
+// far beyond the few microseconds the other epilogues take.
+constexpr int kMaxPolls = 1 << 20;
 __device__ __forceinline__ int ticket(int* ctr) {
   return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -478,17 +488,33 @@ __device__ __forceinline__ void fwd_accumulate(const FwdParams& P, const Hist& H
   }
 }
 
-// Sum of v over the 64 lanes of a wave, in the same butterfly order in every
-// lane (bit-identical result everywhere; float addition is commutative).
+// Sum of v over the 64 lanes of a wave (every lane active), returned in every
+// lane: DPP row shifts by 1, 2, 4 and 8 leave each row's 16-lane total in its
+// lane 15, then the four row totals are read and added in row order -- a fixed
+// order, so the result is bit-identical run to run.  No LDS round trips (a
+// ds_bpermute butterfly costs six of them).
+template <int N>
+__device__ __forceinline__ int row_shr(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0x110 + N, 0xf, 0xf, true);
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += __int_as_float(row_shr<1>(__float_as_int(v)));
+  v += __int_as_float(row_shr<2>(__float_as_int(v)));
+  v += __int_as_float(row_shr<4>(__float_as_int(v)));
+  v += __int_as_float(row_shr<8>(__float_as_int(v)));
+  const int b = __float_as_int(v);
+  return ((__int_as_float(__builtin_amdgcn_readlane(b, 15)) +
+           __int_as_float(__builtin_amdgcn_readlane(b, 31))) +
+          __int_as_float(__builtin_amdgcn_readlane(b, 47))) +
+         __int_as_float(__builtin_amdgcn_readlane(b, 63));
 }
 __device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += row_shr<1>(v);
+  v += row_shr<2>(v);
+  v += row_shr<4>(v);
+  v += row_shr<8>(v);
+  return __builtin_amdgcn_readlane(v, 15) + __builtin_amdgcn_readlane(v, 31) +
+         __builtin_amdgcn_readlane(v, 47) + __builtin_amdgcn_readlane(v, 63);
 }
 
 // Ticket counter i of the workspace (counters are kCtrStride ints apart).
@@ -512,24 +538,23 @@ __device__ __forceinline__ int* counter(const FwdParams& P, int64_t i) {
 // float32 per voxel: a ~1e-7 relative difference per voxel).
 __device__ __forceinline__ void moment_terms(double n, double g, double s1, double s2, double sg,
                                              double cl, double cr, double* out) {
-  const double S = cr - cl;
-  out[0] = (cr * n - s1) / S;
-  out[1] = (s1 - cl * n) / S;
-  out[2] = (cr * s1 - s2) / S;
-  out[3] = (s2 - cl * s1) / S;
-  out[4] = (cr * g - sg) / S;
-  out[5] = (sg - cl * g) / S;
+  const double inv = 1.0 / (cr - cl);
+  out[0] = (cr * n - s1) * inv;
+  out[1] = (s1 - cl * n) * inv;
+  out[2] = (cr * s1 - s2) * inv;
+  out[3] = (s2 - cl * s1) * inv;
+  out[4] = (cr * g - sg) * inv;
+  out[5] = (sg - cl * g) * inv;
 }
 
 // Epilogue of batch indices [b0, b0 + nb) in one block.  Final sums -> W, P,
 // G per bin, d = P/W - G/W (kernels/epilogue.py:23-82); per class row: K_ne,
-// f, coef, jac (one wave per row).  It leaves its final sums zero.  With
-// `loss` (nb == B: the block holds every row) it also sums the per-class
-// errors into the loss, in row order.
+// f, coef, jac (one wave per row).  It leaves its final sums zero and returns
+// (in thread 0, unless the reduction is "none") the sum of its rows'
+// per-class errors in row order.
 template <bool SOFT, bool MOM>
-__device__ __forceinline__ void epilogue(const FwdParams& P, unsigned char* hist,
-                                         const float* repl, int CK, int CL, int b0, int nb,
-                                         bool loss) {
+__device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* hist,
+                                          const float* repl, int CK, int CL, int b0, int nb) {
   const int tid = threadIdx.x;
   const int K = P.K;
   const int NV = fin_values(CK, MOM);
@@ -671,24 +696,18 @@ __device__ __forceinline__ void epilogue(const FwdParams& P, unsigned char* hist
       float jac = P.ignore_empty ? present * w : w;
       if (P.red == kRedMean) jac = jac / (float)rows;
       const int gi = (b0 + bb) * CL + cl;
-      if (loss) {
-        P.f[gi] = fw;
-        sf[row] = fw;
-      } else {
-        store_dev(&P.f[gi], fw);
-      }
+      P.f[gi] = fw;
+      sf[row] = fw;
       P.jac[gi] = jac;
     }
   }
-  if (loss && P.red != kRedNone) {
+  float total = 0.0f;
+  if (P.red != kRedNone) {
     __syncthreads();
-    if (tid == 0) {
-      float total = 0.0f;
-      for (int r = 0; r < rows; ++r) total += sf[r];
-      if (P.red == kRedMean) total = total / (float)rows;
-      P.loss[0] = total;
-    }
+    if (tid == 0)
+      for (int r = 0; r < nb * CL; ++r) total += sf[r];
   }
+  return total;
 }
 
 // Block sums: one lane per bin (half-bin for moments) loads the R copies of
@@ -825,8 +844,8 @@ __device__ __forceinline__ void block_sums(const FwdParams& P, const Hist& H, in
 // (tile % reps) of batch b's final sums (fixed point: exact and
 // order-independent).  Ticket counters, each on its own 256-byte line, then
 // pick the last block of each group of gs tiles, the last group of batch b
-// (which runs b's epilogue) and the last batch (which sums the per-class
-// errors into the loss in a fixed order).
+// (which runs b's epilogue) and the last batch epilogue to start (which sums
+// the per-class errors into the loss in a fixed order).
 template <bool SOFT, bool MOM>
 __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, unsigned char* hist,
                                            const float* repl, int CK, int CL, int b,
@@ -859,38 +878,52 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
   }
   __syncthreads();
   if (!s_last) return;
+  const int rows = P.B * CL;
   if (P.epi_all) {
-    epilogue<SOFT, MOM>(P, hist, repl, CK, CL, 0, P.B, true);
+    const float total = epilogue<SOFT, MOM>(P, hist, repl, CK, CL, 0, P.B);
+    if (tid == 0 && P.red != kRedNone)
+      P.loss[0] = P.red == kRedMean ? total / (float)rows : total;
     return;
   }
-  epilogue<SOFT, MOM>(P, hist, repl, CK, CL, b, 1, false);
-  if (P.red == kRedNone) return;
-
-  // ---- loss: the last batch epilogue sums the B x C' per-class errors
-  wait_own_writes();
-  __syncthreads();
-  if (tid == 0) {
-    int* tc = counter(P, (int64_t)P.B * P.gpb + P.B);
-    const int last = ticket(tc) == P.B - 1;
-    if (last) __hip_atomic_store(tc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last;
+  // ---- loss.  The loss ticket is drawn as b's epilogue starts, so that its
+  // round trip overlaps the epilogue's loads; the block that draws the last
+  // one sums the loss.  Every other batch epilogue publishes its partial sum
+  // as one word (flag bit 32 | float bits) -- no wait for its own writes, no
+  // second ticket -- and the last block polls those words.  The blocks it
+  // waits for drew their tickets earlier and run epilogues that wait on
+  // nothing, so the wait ends; it is bounded all the same (kMaxPolls, then
+  // the loss is NaN).
+  int lt = 0;
+  int* tc = counter(P, (int64_t)P.B * P.gpb + P.B);
+  if (tid == 0 && P.red != kRedNone) lt = ticket(tc);
+  const float total = epilogue<SOFT, MOM>(P, hist, repl, CK, CL, b, 1);
+  if (P.red == kRedNone || tid >= 64) return;
+  // wave 0, every lane active: thread 0's ticket and partial sum
+  const bool last = __builtin_amdgcn_readfirstlane(lt) == P.B - 1;
+  const float own = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(total)));
+  if (!last) {
+    if (tid == 0) store_dev(&P.part[b], (1ull << 32) | (unsigned long long)__float_as_uint(own));
+    return;
   }
-  __syncthreads();
-  if (!s_last) return;
-  const int rows = P.B * CL;
-  float part = 0.0f;
-  for (int i = tid; i < rows; i += kThreads) part += load_dev(&P.f[i]);
-  part = wave_sum(part);
-  float* sp = reinterpret_cast<float*>(hist);
-  if ((tid & 63) == 0) sp[tid >> 6] = part;
-  __syncthreads();
-  if (tid == 0) {
-    float total = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) total += sp[w];
-    if (P.red == kRedMean) total = total / (float)rows;
-    P.loss[0] = total;
+  if (tid == 0) __hip_atomic_store(tc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float sum = 0.0f;
+  for (int c0 = 0; c0 < P.B; c0 += 64) {
+    const int bb = c0 + tid;
+    float v = 0.0f;
+    if (bb == b) {
+      v = own;
+    } else if (bb < P.B) {
+      unsigned long long w = load_dev(&P.part[bb]);
+      for (int n = 0; (w >> 32) == 0 && n < kMaxPolls; ++n) {
+        __builtin_amdgcn_s_sleep(2);
+        w = load_dev(&P.part[bb]);
+      }
+      v = (w >> 32) ? __uint_as_float((unsigned)w) : __builtin_nanf("");
+      store_dev(&P.part[bb], 0ull);
+    }
+    sum += wave_sum(v);
   }
+  if (tid == 0) P.loss[0] = P.red == kRedMean ? sum / (float)rows : sum;
 }
 
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
@@ -1251,8 +1284,8 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         if (c == 0 && skip0) continue;
-        const int k = bucket<RIGHT, false>(p[c], nf, K, tab);
-        const uint32_t q = (uint32_t)rintf(p[c] * 1073741824.0f);
+        const int k = bucket_unit<RIGHT>(p[c], nf, tab);
+        const uint32_t q = fixq(p[c]);
         const uint32_t hi = (lab == (uint32_t)c) ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
                                                  : (1u << (kShiftN - 32));
         lds_add(bin_at(hb[c], k, lsh), ((unsigned long long)hi << 32) | q);
@@ -1265,8 +1298,8 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         if (c == 0 && skip0) continue;
-        const int h = bucket<RIGHT, false>(p[c], nf, 2 * K, tab);
-        const uint32_t q = (uint32_t)rintf(p[c] * 1073741824.0f);
+        const int h = bucket_unit<RIGHT>(p[c], nf, tab);
+        const uint32_t q = fixq(p[c]);
         // the square of the quantised p (q 2^-30), exact in 64 bits, rounded
         // to the same fixed point: the moments then describe one set of
         // values (a float32 p * p would carry a 2^-24 relative error that the
@@ -1438,10 +1471,10 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
       if (c == 0 && off != 0) continue;
       const int cl = c - off;
       if constexpr (!SOFT) {
-        const int k = bucket<RIGHT, false>(p[c], nf, K, tab);
+        const int k = bucket_unit<RIGHT>(p[c], nf, tab);
         gp[c] = scoef[cl * K + k] * sg[cl];
       } else {
-        const int h = bucket<RIGHT, false>(p[c], nf, 2 * K, tab);
+        const int h = bucket_unit<RIGHT>(p[c], nf, tab);
         const float2 ab = *reinterpret_cast<const float2*>(sab + 2 * (cl * 2 * K + h));
         const float y = lab == (uint32_t)c ? 0.5f : 0.0f;
         gp[c] = fmaf(ab.y, p[c] - y, ab.x);

@@ -93,6 +93,7 @@ struct Geometry {
   size_t tab_floats;   // padded bucket table (n + 2) + centre table (2K + 2)
   size_t lds_fwd;      // dynamic LDS of the forward kernel
   size_t lds_bwd;      // dynamic LDS of the backward kernel
+  size_t off_part;     // byte offset of the per-batch loss partial words
   size_t off_fin;      // byte offset of the final sums in the workspace
   size_t ws_bytes;     // workspace bytes; all of it starts zero and is left zero
 };
@@ -169,10 +170,12 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   // soft moments)
   g.lds_bwd = g.tab_floats * 4 +
               align_up((size_t)g.ck * (soft ? 2 : 1) + ((g.CL + 1) & ~1) + (moments ? 4 * g.ck : 0), 4) * 4;
-  // workspace: ticket counters (groups, batch indices, loss) and the final
-  // sums; it must start zero and every call leaves it zero
+  // workspace: ticket counters (groups, batch indices, loss), one loss
+  // partial word per batch index and the final sums; it must start zero and
+  // every call leaves it zero
   const int64_t counters = B * g.gpb + B + 1;
-  g.off_fin = align_up((size_t)counters * kCtrStride * sizeof(int), 256);
+  g.off_part = align_up((size_t)counters * kCtrStride * sizeof(int), 256);
+  g.off_fin = align_up(g.off_part + (size_t)B * sizeof(unsigned long long), 256);
   const size_t fin_bytes = (size_t)B * g.reps * fin_values(g.ck, moments) * sizeof(unsigned long long);
   g.ws_bytes = align_up(g.off_fin + fin_bytes, 256);
   return g;

@@ -93,16 +93,25 @@ long long check_range(const float* table, int n, int right, float lo, float hi) 
   return bad;
 }
 
-// bucket<RIGHT, false> (no input clamp, the softmax path) at every float32 in
-// [lo, hi] within [0, 1], and at every float32 of [0, 1] within `ulps` of an
-// edge when ulps > 0 (lo, hi then ignored).
-long long check_unclamped(const float* table, int n, int right, float lo, float hi, int ulps) {
+// bucket_unit<RIGHT> (probabilities in [0, 1], one correction: the softmax
+// path) at every float32 in [lo, hi] within [0, 1], and at every float32 of
+// [0, 1] within `ulps` of an edge when ulps > 0 (lo, hi then ignored).
+// planted != 0 drops the correction (the first guess alone): the sweep must
+// then find mismatches.
+long long check_unit(const float* table, int n, int right, float lo, float hi, int ulps,
+                     int planted) {
   const std::vector<float> tab = padded(table, n);
   auto one = [&](float p) -> long long {
     int want = expected(table, n, p, right != 0);
     if (want > n - 1) want = n - 1;
-    const int k = right ? ace::bucket<true, false>(p, (float)n, n, tab.data())
-                        : ace::bucket<false, false>(p, (float)n, n, tab.data());
+    int k;
+    if (planted) {
+      const float t = std::fmaf(p, (float)n, -0.25f);
+      k = (int)t;
+    } else {
+      k = right ? ace::bucket_unit<true>(p, (float)n, tab.data())
+                : ace::bucket_unit<false>(p, (float)n, tab.data());
+    }
     return k != want ? 1 : 0;
   };
   long long bad = 0;
@@ -126,12 +135,44 @@ long long check_unclamped(const float* table, int n, int right, float lo, float 
   return bad;
 }
 
-// bucket<RIGHT, false> of a NaN (NaN logits) is 0, inside the histogram.
-int check_unclamped_nan(const float* table, int n) {
+// ace::div_rn(a, b, 1 / b) against a / b: every float b with bits in
+// [b_lo, b_hi) times `per_b` pseudo-random a of exponents in [ea, eb] (plus
+// a = 1 and a = b / 2).  Returns the mismatches.  planted != 0 checks a * y
+// instead (no residual correction): the check must then report mismatches.
+long long check_div(uint32_t b_lo, uint32_t b_hi, int per_b, int ea, int eb, int planted) {
+  long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+  for (int64_t u = b_lo; u < (int64_t)b_hi; ++u) {
+    const float b = from_bits((uint32_t)u);
+    const float y = 1.0f / b;
+    uint32_t h = (uint32_t)u * 2654435761u;
+    for (int t = 0; t < per_b + 2; ++t) {
+      h ^= h >> 15;
+      h *= 0x2c1b3c6dU;
+      h ^= h >> 12;
+      h *= 0x297a2d39U;
+      h ^= h >> 15;
+      float a;
+      if (t == 0) {
+        a = 1.0f;
+      } else if (t == 1) {
+        a = b * 0.5f;
+      } else {
+        const int e = ea + (int)(h % (uint32_t)(eb - ea + 1));
+        a = std::ldexp(1.0f + (float)(h >> 9) * (1.0f / 8388608.0f), e);
+      }
+      if ((planted ? a * y : ace::div_rn(a, b, y)) != a / b) ++bad;
+    }
+  }
+  return bad;
+}
+
+// bucket_unit of a NaN (NaN logits) is 0, inside the histogram.
+int check_unit_nan(const float* table, int n) {
   const std::vector<float> tab = padded(table, n);
   const float q = std::nanf("");
-  return ace::bucket<false, false>(q, (float)n, n, tab.data()) == 0 &&
-         ace::bucket<true, false>(q, (float)n, n, tab.data()) == 0;
+  return ace::bucket_unit<false>(q, (float)n, tab.data()) == 0 &&
+         ace::bucket_unit<true>(q, (float)n, tab.data()) == 0;
 }
 
 // Planted mistake for the sensitivity test: the first guess floor(p * n)

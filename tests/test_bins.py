@@ -12,8 +12,10 @@ against a binary search over the same float32 ``torch.linspace`` tables:
 - every float32 in [0, 1 + eps32] (exhaustive) for the benchmark tables
   K = 20 and K = 50;
 - out-of-domain values (NaN, +-inf, > 1) stay inside [0, n - 1];
-- the softmax variant without input clamp (``bucket<RIGHT, false>``) on every
-  float32 of [0, 1] for K = 20 and 50, near every edge for every K, and NaN.
+- the softmax variant for probabilities in [0, 1] (``bucket_unit``: first
+  guess trunc(p * n - 1/4), one correction) on every float32 of [0, 1] for
+  K = 20 and 50, near every edge for every K, NaN, and with its correction
+  dropped (a planted mistake the near-edge sweep must catch).
 """
 
 from __future__ import annotations
@@ -47,11 +49,14 @@ def harness(tmp_path_factory) -> ctypes.CDLL:
     lib.check_range.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float]
     lib.check_clamped.restype = ctypes.c_int
     lib.check_clamped.argtypes = [fp, ctypes.c_int]
-    lib.check_unclamped.restype = ctypes.c_longlong
-    lib.check_unclamped.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
-                                    ctypes.c_int]
-    lib.check_unclamped_nan.restype = ctypes.c_int
-    lib.check_unclamped_nan.argtypes = [fp, ctypes.c_int]
+    lib.check_unit.restype = ctypes.c_longlong
+    lib.check_unit.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                               ctypes.c_int, ctypes.c_int]
+    lib.check_div.restype = ctypes.c_longlong
+    lib.check_div.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                              ctypes.c_int]
+    lib.check_unit_nan.restype = ctypes.c_int
+    lib.check_unit_nan.argtypes = [fp, ctypes.c_int]
     return lib
 
 
@@ -112,19 +117,51 @@ def test_edges_detect_an_uncorrected_index(harness) -> None:
 
 
 @pytest.mark.parametrize("soft", [False, True])
-def test_unclamped_softmax_variant(harness, soft: bool) -> None:
-    """bucket<RIGHT, false>, used on softmax probabilities: exhaustive on [0, 1]
+def test_unit_interval_variant(harness, soft: bool) -> None:
+    """bucket_unit<RIGHT>, used on softmax probabilities: exhaustive on [0, 1]
     for the benchmark tables, near every edge for every K, NaN -> bin 0."""
     for k in (20, 50):
         t = _table(k, soft)
         for right in (0, 1):
-            assert harness.check_unclamped(_fp(t), t.size, right, 0.0, 1.0, 0) == 0
+            assert harness.check_unit(_fp(t), t.size, right, 0.0, 1.0, 0, 0) == 0
     bad = {}
     for k in KS:
         t = _table(k, soft)
         for right in (0, 1):
-            n = harness.check_unclamped(_fp(t), t.size, right, 0.0, 0.0, 4096)
+            n = harness.check_unit(_fp(t), t.size, right, 0.0, 0.0, 4096, 0)
             if n:
                 bad[(k, right)] = n
-        assert harness.check_unclamped_nan(_fp(t), t.size) == 1
+        assert harness.check_unit_nan(_fp(t), t.size) == 1
     assert not bad, bad
+
+
+def test_unit_interval_variant_needs_its_correction(harness) -> None:
+    """Planted mistake: the first guess trunc(p * n - 1/4) alone must fail near
+    edges (it is k - 1 just above every edge), so the sweep above would catch a
+    lost correction."""
+    total = 0
+    for k in (3, 7, 20, 50):
+        t = _table(k, False)
+        for right in (0, 1):
+            total += harness.check_unit(_fp(t), t.size, right, 0.0, 0.0, 8, 1)
+    assert total > 0
+
+
+def _bits(v: float) -> int:
+    return int(np.array([v], dtype=np.float32).view(np.uint32)[0])
+
+
+def test_division_from_rounded_reciprocal(harness) -> None:
+    """div_rn(a, b, RN(1/b)) is the IEEE quotient: every float b in [1, 16)
+    (softmax sums) with 4 random a of exponents -100..0 each, and a sample of
+    spans b in [2^-20, 2^14) with a of exponents -40..14."""
+    assert harness.check_div(_bits(1.0), _bits(16.0), 4, -100, 0, 0) == 0
+    lo, hi = _bits(2.0 ** -20), _bits(2.0 ** 14)
+    for start in range(lo, hi, (hi - lo) // 16):
+        assert harness.check_div(start, min(start + (1 << 18), hi), 4, -40, 14, 0) == 0
+
+
+def test_division_check_catches_a_missing_correction(harness) -> None:
+    """Planted mistake: a * RN(1/b) without the residual correction is wrong
+    for some a, and the check above reports it."""
+    assert harness.check_div(_bits(1.0), _bits(1.0) + (1 << 16), 4, -30, 0, 1) > 0
