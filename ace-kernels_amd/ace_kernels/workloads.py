@@ -14,6 +14,12 @@ labels (``to_onehot_y=True``, softmax), generated on the CPU with a seeded
 5. soft, K=50, bfloat16 x[32,4,512,512] ~ N(0, 1); labels uniform in [0,4);
    +1.5 for 60%; background excluded from the loss
 
+Deep supervision (``deep_supervision(binning)``): the four output levels of
+SegResNetDS at a 128^3 patch -- x[1,4,s,s,s] for s = 128, 64, 32, 16, one loss
+call per level and one backward through their sum per step (the reference's
+``bench/configs/sprint11_deepsup.yaml``, shapes ds0-128 ... ds3-16), with the
+distribution of configuration 2.
+
 "N(0, s)" is read with s the standard deviation (``randn * scale``), as the
 reference's ``make_inputs`` (``src/ace_kernels/cases.py:60-63``); the bias is
 added on the label channel with ``scatter_add`` like ``cases.py:90-93``, under
@@ -103,6 +109,16 @@ WORKLOADS: Dict[int, Workload] = {
     5: Workload(5, "cfg5-soft-K50-32x4x512^2-bf16-nobg", 32, 4, (512, 512), 1.0, (0.25,) * 4, 1.5, 0.60,
                 torch.bfloat16, _paper(binning="soft", num_bins=50, include_background=False), seed=5),
 }
+
+
+def deep_supervision(binning: str) -> List[Workload]:
+    """The four levels of the deep-supervision step (128^3 ... 16^3, B=1, C=4)."""
+    out = []
+    for level, side in enumerate((128, 64, 32, 16)):
+        out.append(Workload(100 + level, f"ds{level}-{side}-{binning}", 1, 4, (side,) * 3, 1.5,
+                            (0.90, 0.06, 0.03, 0.01), 2.5, 0.80, torch.float32,
+                            _paper(binning=binning, num_bins=20), seed=20 + level))
+    return out
 
 
 def workload(index: int) -> Workload:

@@ -195,6 +195,62 @@ def bench_workload(wl, steps: int, warmup: int, flush):
     return out
 
 
+def bench_deep_supervision(binning: str, steps: int, warmup: int, flush):
+    """Deep-supervision step: one loss call per level (128^3 ... 16^3, B=1) and
+    one backward through the sum of the four losses; eager and HIP-graph
+    replay, plus each level's own fwd+bwd step."""
+    import torch
+
+    from ace_kernels import ace_loss
+    from ace_kernels.workloads import deep_supervision
+
+    levels = deep_supervision(binning)
+    data = []
+    for wl in levels:
+        x, y = wl.make("cuda")
+        data.append((x.requires_grad_(True), y, wl.config))
+    xs = [d[0] for d in data]
+
+    def step():
+        total = sum(ace_loss(x, y, cfg, impl="hip_mi355x") for x, y, cfg in data)
+        return torch.autograd.grad(total, xs)
+
+    eager = time_steps(step, steps, warmup, flush)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        g_static = step()
+    graph.replay()
+    torch.cuda.synchronize()
+    g_eager = step()
+    torch.cuda.synchronize()
+    graph_ok = all(bool(torch.equal(a, b)) for a, b in zip(g_static, g_eager))
+    graphed = time_steps(graph.replay, steps, warmup, flush)
+    del graph
+    per_level = {}
+    for wl, (x, y, cfg) in zip(levels, data):
+        def one(x=x, y=y, cfg=cfg):
+            return torch.autograd.grad(ace_loss(x, y, cfg, impl="hip_mi355x").sum(), x)
+        per_level[wl.name] = _quantiles(time_steps(one, steps, warmup, flush))["p50"]
+    ideal = sum(wl.ideal_bytes("fwd_bwd") for wl in levels)
+    return {
+        "binning": binning,
+        "levels": [wl.name for wl in levels],
+        "ideal_bytes_fwd_bwd": ideal,
+        "eager_ms": _quantiles(eager),
+        "graph_ms": _quantiles(graphed),
+        "graph_replay_matches_eager": graph_ok,
+        "level_eager_ms_p50": per_level,
+        "pct_hbm_peak": 100.0 * ideal / (_quantiles(eager)["p50"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+    }
+
+
 def cpu_baseline(budget_s: float = 15.0):
     """The reference algorithm (oracle restatement, torch CPU) fwd+bwd on the
     benchmark workload (configuration 2), a bounded number of calls."""
@@ -286,6 +342,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--workloads", default="2,3", help="benchmark workloads (first = value)")
+    ap.add_argument("--no-deepsup", action="store_true", help="skip the deep-supervision steps")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="LAUNCHES",
                     help="only launch the kernels LAUNCHES times each (for rocprofv3)")
     args = ap.parse_args()
@@ -311,6 +368,12 @@ def main() -> int:
         log(f"bench {wl.name}: steps={args.steps} warmup={args.warmup}")
         results.append(bench_workload(wl, args.steps, args.warmup, flush))
         log(json.dumps(results[-1]))
+    deepsup = []
+    if not args.no_deepsup:
+        for binning in ("hard", "soft"):
+            log(f"bench deep supervision {binning}")
+            deepsup.append(bench_deep_supervision(binning, args.steps, args.warmup, flush))
+            log(json.dumps(deepsup[-1]))
     main_r = results[0]
     dom = main_r["dominant"]
     achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
@@ -353,6 +416,7 @@ def main() -> int:
             "ms_mean": dom["ms"],
         },
         "workloads": results,
+        "deep_supervision": deepsup,
     }
     if not args.no_cpu:
         log("cpu baseline (oracle reference, cfg1)")
