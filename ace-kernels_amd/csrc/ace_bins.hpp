@@ -62,17 +62,25 @@ ACE_HD float div_rn(float a, float b, float y) {
 // g <= n - 1 for p <= 1, and e_{n-1} = 1 + eps > 1, so no clamp is needed.
 // tab is the padded table (tab[j + 1] = e_j).  NaN bins to 0: the device
 // conversion is v_cvt_i32_f32, which maps NaN to 0.
-template <bool RIGHT>
-ACE_HD int bucket_unit(float p, float nf, const float* tab) {
+ACE_HD int bucket_guess(float p, float nf) {
   const float t = fmaf(p, nf, -0.25f);
 #if defined(__HIP_DEVICE_COMPILE__)
   int g;
   asm("v_cvt_i32_f32 %0, %1" : "=v"(g) : "v"(t));
+  return g;
 #else
-  const int g = t == t ? (int)t : 0;
+  return t == t ? (int)t : 0;
 #endif
-  const float e = tab[g + 1];
+}
+// e = tab[g + 1], the upper edge of bin g.
+template <bool RIGHT>
+ACE_HD int bucket_fix(int g, float e, float p) {
   return g + ((RIGHT ? (e <= p) : (e < p)) ? 1 : 0);
+}
+template <bool RIGHT>
+ACE_HD int bucket_unit(float p, float nf, const float* tab) {
+  const int g = bucket_guess(p, nf);
+  return bucket_fix<RIGHT>(g, tab[g + 1], p);
 }
 
 }  // namespace ace

@@ -199,22 +199,21 @@ __device__ __forceinline__ uint32_t fixq(float p) {
 
 // ------------------------------------------------------------ activation
 
-// exp(x) for the softmax arguments x = logit - max <= 0: 2^(x log2 e) with the
-// usual split of x log2 e into ph + pl (log2 e rounded to float, the product's
-// rounding error by fma, plus x times the remainder of log2 e), the integer
-// part of ph taken out by rint/ldexp so that v_exp_f32 sees a reduced argument
-// that carries pl.  This is the range reduction ROCm's expf uses; its
-// overflow/underflow selects are replaced by one clamp of x at -104, below
-// which every result underflows (x <= 0 cannot overflow).  Measured on MI355X
-// against a float64 exp for every float x in [-104, 0]: max error 0.857 ulp,
-// no result off by more than 1 ulp -- the same figures as ROCm's expf.
+// exp(x) for the softmax arguments x = logit - max <= 0: 2^(x log2 e) with
+// e = rint(x log2 e) taken out by ldexp and the reduced argument
+// a = x log2 e - e formed with one fma (exact product, one rounding: |a| <=
+// 1/2, so its rounding error is ~2^-26) plus x times the remainder of log2 e
+// (log2 e = L + Llo, L its float rounding).  v_exp_f32 then sees a in
+// [-1/2, 1/2].  A clamp of x at -104, below which every result underflows,
+// keeps -inf logits finite (x <= 0 cannot overflow).  Measured on MI355X
+// against a float64 exp for every float x in [-104, 0]: max error 0.968 ulp,
+// no result off by more than 1 ulp (ROCm's expf: 0.857 / none; its range
+// reduction splits x log2 e into two terms first, two instructions more).
 __device__ __forceinline__ float exp_neg(float x) {
   x = fmaxf(x, -104.0f);
-  const float ph = x * 0x1.715476p+0f;
-  float pl = fmaf(x, 0x1.715476p+0f, -ph);
-  pl = fmaf(x, 0x1.4ae0bep-26f, pl);
-  const float e = rintf(ph);
-  const float a = (ph - e) + pl;
+  const float e = rintf(x * 0x1.715476p+0f);
+  float a = fmaf(x, 0x1.715476p+0f, -e);
+  a = fmaf(x, 0x1.4ae0bep-26f, a);
   return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(a), (int)e);
 }
 
@@ -1273,48 +1272,77 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
                                                 unsigned long long* const (&hb)[C],
                                                 const size_t words) {
   const float nf = (float)(SOFT ? 2 * K : K);
+  // C <= 4: all VEC voxels at a time -- every bin guess first, then every
+  // table read, then the corrections and atomics.  The table reads cannot
+  // move past an LDS atomic (same LDS array), so this order keeps VEC * C
+  // reads in flight instead of waiting for each one; the blocks are all
+  // resident at 4 waves per SIMD, so up to 128 registers per lane cost
+  // nothing.  C = 16: one voxel at a time, each table read just before its
+  // use (the batched form would need more than 128 registers).
+  constexpr bool BATCH = C <= 4;
+  constexpr int NJ = BATCH ? VEC : 1;
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) {
-    float p[C];
+  for (int j0 = 0; j0 < VEC; j0 += NJ) {
+    float p[NJ][C];
+    uint32_t lab[NJ];
+    int g[NJ][C];
+    float e[NJ][C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) p[c] = t.x[c][j];
-    softmax_fast<C>(p);
-    const uint32_t lab = fast_label<C>(t.lab[j]);
-    if constexpr (!SOFT) {
+    for (int jj = 0; jj < NJ; ++jj) {
 #pragma unroll
-      for (int c = 0; c < C; ++c) {
-        if (c == 0 && skip0) continue;
-        const int k = bucket_unit<RIGHT>(p[c], nf, tab);
-        const uint32_t q = fixq(p[c]);
-        const uint32_t hi = (lab == (uint32_t)c) ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
-                                                 : (1u << (kShiftN - 32));
-        lds_add(bin_at(hb[c], k, lsh), ((unsigned long long)hi << 32) | q);
+      for (int c = 0; c < C; ++c) p[jj][c] = t.x[c][j0 + jj];
+      softmax_fast<C>(p[jj]);
+      lab[jj] = fast_label<C>(t.lab[j0 + jj]);
+#pragma unroll
+      for (int c = 0; c < C; ++c) g[jj][c] = bucket_guess(p[jj][c], nf);
+    }
+    if constexpr (BATCH) {
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+          if (!(c == 0 && skip0)) e[jj][c] = tab[g[jj][c] + 1];
+    }
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      if constexpr (!SOFT) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          if (c == 0 && skip0) continue;
+          const int k = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
+          const uint32_t q = fixq(p[jj][c]);
+          const uint32_t hi = (lab[jj] == (uint32_t)c)
+                                  ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
+                                  : (1u << (kShiftN - 32));
+          lds_add(bin_at(hb[c], k, lsh), ((unsigned long long)hi << 32) | q);
+        }
+      } else {
+        // soft: moments of the voxel's half-bin h (count | labelled count |
+        // sum p packed as in hard binning, sum p^2, labelled sum p)
+        unsigned long long* ga = hb[0];
+        uint32_t gq = 0u;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          if (c == 0 && skip0) continue;
+          const int h = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
+          const uint32_t q = fixq(p[jj][c]);
+          // the square of the quantised p (q 2^-30), exact in 64 bits,
+          // rounded to the same fixed point: the moments then describe one
+          // set of values (a float32 p * p would carry a 2^-24 relative
+          // error that the moment formulas amplify by 1 / S)
+          const uint32_t q2 = (uint32_t)(((unsigned long long)q * q + (1ull << 29)) >> 30);
+          const bool hit = lab[jj] == (uint32_t)c;
+          const uint32_t hi = hit ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
+                                  : (1u << (kShiftN - 32));
+          unsigned long long* a = bin_at(hb[c], h, lsh);
+          lds_add(a, ((unsigned long long)hi << 32) | q);
+          lds_add(a + words, (unsigned long long)q2);
+          ga = hit ? a : ga;
+          gq = hit ? q : gq;
+        }
+        if (lab[jj] != 0xffffffffu && !(lab[jj] == 0u && skip0))
+          lds_add(ga + 2 * words, (unsigned long long)gq);
       }
-    } else {
-      // soft: moments of the voxel's half-bin h (count | labelled count |
-      // sum p packed as in hard binning, sum p^2, labelled sum p)
-      unsigned long long* ga = hb[0];
-      uint32_t gq = 0u;
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        if (c == 0 && skip0) continue;
-        const int h = bucket_unit<RIGHT>(p[c], nf, tab);
-        const uint32_t q = fixq(p[c]);
-        // the square of the quantised p (q 2^-30), exact in 64 bits, rounded
-        // to the same fixed point: the moments then describe one set of
-        // values (a float32 p * p would carry a 2^-24 relative error that the
-        // moment formulas amplify by 1 / S)
-        const uint32_t q2 = (uint32_t)(((unsigned long long)q * q + (1ull << 29)) >> 30);
-        const bool hit = lab == (uint32_t)c;
-        const uint32_t hi = hit ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
-                                : (1u << (kShiftN - 32));
-        unsigned long long* a = bin_at(hb[c], h, lsh);
-        lds_add(a, ((unsigned long long)hi << 32) | q);
-        lds_add(a + words, (unsigned long long)q2);
-        ga = hit ? a : ga;
-        gq = hit ? q : gq;
-      }
-      if (lab != 0xffffffffu && !(lab == 0u && skip0)) lds_add(ga + 2 * words, (unsigned long long)gq);
     }
   }
 }

@@ -251,6 +251,33 @@ def bench_deep_supervision(binning: str, steps: int, warmup: int, flush):
     }
 
 
+def hard_bin_parity(wl):
+    """Per-bin counts of the HIP forward against torch's CPU softmax +
+    torch.bucketize on the same inputs and float32 edges: voxels within one
+    ulp of an edge (where the reference's own bin is rounding-dependent) and
+    voxels whose bin differs (must not exceed the former)."""
+    import torch
+
+    from ace_kernels.common import bin_tables
+    from ace_kernels.impls import hip_mi355x as hip
+
+    cfg = wl.config
+    x, y = wl.make("cpu")
+    st = hip.hip_forward(hip.make_plan(x.cuda(), y.cuda(), cfg), cfg, stats=True)[5]
+    w_gpu = st[0].cpu()
+    p = torch.softmax(x, 1).reshape(x.shape[0], x.shape[1], -1)
+    edges, _ = bin_tables(cfg.num_bins, False, torch.device("cpu"))
+    k = cfg.num_bins
+    bins = torch.bucketize(p, edges, right=cfg.right).clamp_(max=k - 1)
+    down = torch.bucketize(torch.nextafter(p, torch.tensor(-1.0)), edges, right=cfg.right)
+    up = torch.bucketize(torch.nextafter(p, torch.tensor(2.0)), edges, right=cfg.right)
+    w_cpu = torch.zeros(x.shape[0], x.shape[1], k, dtype=torch.float64)
+    w_cpu.scatter_add_(2, bins, torch.ones_like(bins, dtype=torch.float64))
+    moved = int((w_gpu - w_cpu).abs().sum().item() / 2)
+    return {"workload": wl.name, "channel_voxels": p.numel(),
+            "within_one_ulp_of_an_edge": int((down != up).sum().item()), "moved": moved}
+
+
 def cpu_baseline(budget_s: float = 15.0):
     """The reference algorithm (oracle restatement, torch CPU) fwd+bwd on the
     benchmark workload (configuration 2), a bounded number of calls."""
@@ -374,6 +401,11 @@ def main() -> int:
             log(f"bench deep supervision {binning}")
             deepsup.append(bench_deep_supervision(binning, args.steps, args.warmup, flush))
             log(json.dumps(deepsup[-1]))
+    parity = None
+    first = workload(int(args.workloads.split(",")[0]))
+    if first.config.binning == "hard":
+        log("hard-bin parity against torch.bucketize")
+        parity = hard_bin_parity(first)
     main_r = results[0]
     dom = main_r["dominant"]
     achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
@@ -417,6 +449,7 @@ def main() -> int:
         },
         "workloads": results,
         "deep_supervision": deepsup,
+        "hard_bin_parity": parity,
     }
     if not args.no_cpu:
         log("cpu baseline (oracle reference, cfg1)")
