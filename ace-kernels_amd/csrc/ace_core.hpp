@@ -573,7 +573,7 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
     // its six contributions
     const int H2 = 2 * CK;
     for (int t = tid; t < nb * H2; t += kThreads) {
-      const int bb = t / H2;
+      const int bb = nb == 1 ? 0 : t / H2;
       const int th = t - bb * H2;
       unsigned long long* fb = P.fin + (int64_t)(b0 + bb) * reps * NV;
       long long m[5] = {0, 0, 0, 0, 0};
@@ -597,7 +597,7 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
     __syncthreads();
   }
   for (int i = tid; i < NB; i += kThreads) {
-    const int bb = i / CK;
+    const int bb = nb == 1 ? 0 : i / CK;
     const int t = i - bb * CK;
     double Wd, Pd, Gd;
     if constexpr (MOM) {
@@ -665,28 +665,51 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
   const int rows = P.B * CL;
   for (int row = tid >> 6; row < nb * CL; row += kThreads / 64) {
     const int base = row * K;  // == bb * CK + cl * K
-    const int bb = row / CL;
+    const int bb = nb == 1 ? 0 : row / CL;
     const int cl = row - bb * CL;
-    int kne = 0;
-    float err = 0.0f, gsum = 0.0f;
-    for (int k = lane; k < K; k += 64) {
-      if (!se[base + k]) {
-        ++kne;
-        err += fabsf(sd[base + k]);
-      }
-      gsum += sg[base + k];
-    }
-    kne = wave_sum(kne);
-    err = wave_sum(err);
-    gsum = wave_sum(gsum);
-    const float fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
-    const float present = gsum > 0.0f ? 1.0f : 0.0f;
-    const float kf = (float)(kne > 0 ? kne : 1);
     const int64_t ob = (int64_t)(b0 + bb) * CK + cl * K;
-    for (int k = lane; k < K; k += 64) {
-      const float dd = sd[base + k];
-      const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
-      P.coef[ob + k] = se[base + k] ? 0.0f : sgn / (kf * sw[base + k]);
+    int kne;
+    float fcls, present;
+    if (K <= 64) {
+      // one bin per lane: every LDS value read once, in one round trip
+      const bool in = lane < K;
+      const int i = base + (in ? lane : 0);
+      const float dd = sd[i];
+      const float wv = sw[i];
+      const float gv = sg[i];
+      const bool emp = se[i] != 0;
+      const bool ne = in && !emp;
+      kne = wave_sum(ne ? 1 : 0);
+      const float err = wave_sum(ne ? fabsf(dd) : 0.0f);
+      const float gsum = wave_sum(in ? gv : 0.0f);
+      fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
+      present = gsum > 0.0f ? 1.0f : 0.0f;
+      const float kf = (float)(kne > 0 ? kne : 1);
+      if (in) {
+        const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
+        P.coef[ob + lane] = emp ? 0.0f : sgn / (kf * wv);
+      }
+    } else {
+      kne = 0;
+      float err = 0.0f, gsum = 0.0f;
+      for (int k = lane; k < K; k += 64) {
+        if (!se[base + k]) {
+          ++kne;
+          err += fabsf(sd[base + k]);
+        }
+        gsum += sg[base + k];
+      }
+      kne = wave_sum(kne);
+      err = wave_sum(err);
+      gsum = wave_sum(gsum);
+      fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
+      present = gsum > 0.0f ? 1.0f : 0.0f;
+      const float kf = (float)(kne > 0 ? kne : 1);
+      for (int k = lane; k < K; k += 64) {
+        const float dd = sd[base + k];
+        const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
+        P.coef[ob + k] = se[base + k] ? 0.0f : sgn / (kf * sw[base + k]);
+      }
     }
     if (lane == 0) {
       const float w = P.clsw ? P.clsw[cl] : 1.0f;
