@@ -116,9 +116,13 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   g.ck = g.CL * K;
   g.B = B;
   g.N = N;
-  // histogram copies: up to 32 (lane % 32), within the LDS budget
+  // histogram copies (lane % copies), within the LDS budget: at most 8 for
+  // hard binning and soft moments -- more copies cut LDS address conflicts
+  // but lengthen the block sums, and on MI355X 8 measured fastest for hard
+  // (cfg 2: 8 ~ 16 < 32 copies); soft moments fill the LDS budget at 8 --
+  // and up to 32 for the generic soft sums
   const size_t per_copy = hist_bytes_per_copy(g.ck, soft, labels, moments);
-  int copies = copies_override > 0 ? copies_override : 32;
+  int copies = copies_override > 0 ? copies_override : ((soft && !moments) ? 32 : 8);
   while (copies > 1 && per_copy * copies > (copies_override > 0 ? 160 * 1024 : kMaxHistLds))
     copies /= 2;
   g.copies = copies;
