@@ -679,15 +679,18 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
       const float gv = sg[i];
       const bool emp = se[i] != 0;
       const bool ne = in && !emp;
-      kne = wave_sum(ne ? 1 : 0);
+      kne = __popcll(__ballot(ne));
       const float err = wave_sum(ne ? fabsf(dd) : 0.0f);
       const float gsum = wave_sum(in ? gv : 0.0f);
-      fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
+      // the row's serial tail: v_rcp_f32 (1 ulp) instead of IEEE quotients
+      // for f = mean |d| and coef = sign(d) / (K_ne W), far inside the loss
+      // and gradient tolerances
+      fcls = kne > 0 ? err * __builtin_amdgcn_rcpf((float)kne) : __builtin_nanf("");
       present = gsum > 0.0f ? 1.0f : 0.0f;
       const float kf = (float)(kne > 0 ? kne : 1);
       if (in) {
         const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
-        P.coef[ob + lane] = emp ? 0.0f : sgn / (kf * wv);
+        P.coef[ob + lane] = emp ? 0.0f : sgn * __builtin_amdgcn_rcpf(kf * wv);
       }
     } else {
       kne = 0;
