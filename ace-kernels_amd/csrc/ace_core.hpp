@@ -189,11 +189,12 @@ __device__ __forceinline__ float rcp_rn(float b) {
 }
 // div_rn(a, b, y): ace_bins.hpp (shared with the CPU test harness).
 
-// p in [0, 1] (or NaN) in 30-bit fixed point, truncated: v_cvt_u32_f32 rounds
-// toward zero and maps NaN to 0.  At most 2^-30 below p.
-__device__ __forceinline__ uint32_t fixq(float p) {
+// A probability already scaled by 2^30 (p in [0, 2^30] or NaN) as 30-bit
+// fixed point, truncated: v_cvt_u32_f32 rounds toward zero and maps NaN to
+// 0.  At most 2^-30 below p.
+__device__ __forceinline__ uint32_t cvt_u32(float p30) {
   uint32_t q;
-  asm("v_cvt_u32_f32 %0, %1" : "=v"(q) : "v"(p * 1073741824.0f));
+  asm("v_cvt_u32_f32 %0, %1" : "=v"(q) : "v"(p30));
   return q;
 }
 
@@ -365,17 +366,18 @@ struct TableRegs {
       r[u] = nrepl > 0 ? rtab[min(i, nrepl - 1)] : 0.0f;
     }
   }
+  // bscale: a power of two the bucket table is multiplied by (exact)
   __device__ __forceinline__ void store(float* lds, const float* btab, const float* rtab, int n,
-                                        int nrepl) const {
+                                        int nrepl, float bscale = 1.0f) const {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int i = (int)threadIdx.x + u * kThreads;
-      if (i < n + 2) lds[i] = i == 0 ? -__builtin_inff() : (i <= n ? b[u] : __builtin_inff());
+      if (i < n + 2) lds[i] = i == 0 ? -__builtin_inff() : (i <= n ? b[u] * bscale : __builtin_inff());
       if (i < nrepl) lds[n + 2 + i] = r[u];
     }
     // tables longer than 2 x kThreads entries
     for (int i = (int)threadIdx.x + 2 * kThreads; i < n + 2; i += kThreads)
-      lds[i] = i == n + 1 ? __builtin_inff() : btab[i - 1];
+      lds[i] = i == n + 1 ? __builtin_inff() : btab[i - 1] * bscale;
     for (int i = (int)threadIdx.x + 2 * kThreads; i < nrepl; i += kThreads)
       lds[n + 2 + i] = rtab[i];
   }
@@ -1289,15 +1291,55 @@ __device__ __forceinline__ void softmax_fast(float (&x)[C]) {
   for (int c = 0; c < C; ++c) x[c] = div_rn(x[c], s, y);
 }
 
+// softmax_fast with every probability scaled by 2^30 (the fixed-point scale
+// of the histograms): q = e y 2^30, r = e - (s 2^-30) q, p = q + r y 2^30 are
+// the steps of div_rn with both factors scaled by powers of two, so p is
+// exactly 2^30 times the correctly rounded quotient (tiny quotients below
+// 2^-126 aside, which are bin 0 and 0 in fixed point either way) and one
+// multiply per channel is saved.
+template <int C>
+__device__ __forceinline__ void softmax_fixed(float (&x)[C]) {
+  const float m = max_of<C>(x);
+  x[0] = exp_neg(x[0] - m);
+  float s = x[0];
+#pragma unroll
+  for (int c = 1; c < C; ++c) {
+    x[c] = exp_neg(x[c] - m);
+    s += x[c];
+  }
+  const float y = rcp_rn(s) * 0x1p30f;
+  const float s30 = s * 0x1p-30f;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const float q = x[c] * y;
+    const float r = fmaf(-s30, q, x[c]);
+    x[c] = fmaf(r, y, q);
+  }
+}
+
+// Hard binning, C <= 4: the high word of a voxel's packed increment for
+// channel c is 1 << 21 (count) | (label == c) << 10 (label count).  X holds
+// 0x04 in byte `label` (0 for labels naming no channel); one v_perm_b32 per
+// channel picks that byte into byte 1 and 0x20 from K into byte 2.
+__device__ __forceinline__ uint32_t label_bytes(long long lab, int C) {
+  const unsigned long long u = (unsigned long long)lab;
+  const uint32_t lo = (uint32_t)u;
+  return u < (unsigned long long)C ? (4u << ((lo << 3) & 31)) : 0u;
+}
+__device__ __forceinline__ uint32_t packed_high(uint32_t X, int c) {
+  return __builtin_amdgcn_perm(X, 1u << (kShiftN - 32), 0x0c02040cu + ((uint32_t)c << 8));
+}
+
 // One tile into the histogram copies.  hb[c]: this lane's copy of channel c's
 // bin 0 (u64 words), bins R words = 1 << lsh bytes apart.  skip0: channel 0
 // (background) is not in the loss.
-template <int C, int VEC, bool SOFT, bool RIGHT>
+template <int C, int VEC, bool SOFT, bool RIGHT, bool skip0>
 __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const float* tab,
-                                                const float* repl, int K, bool skip0, int lsh,
+                                                const float* repl, int K, int lsh,
                                                 unsigned long long* const (&hb)[C],
                                                 const size_t words) {
-  const float nf = (float)(SOFT ? 2 * K : K);
+  // probabilities come scaled by 2^30 (softmax_fixed), the bucket table too
+  const float nf = (float)(SOFT ? 2 * K : K) * 0x1p-30f;
   // C <= 4: all VEC voxels at a time -- every bin guess first, then every
   // table read, then the corrections and atomics.  The table reads cannot
   // move past an LDS atomic (same LDS array), so this order keeps VEC * C
@@ -1317,7 +1359,7 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
     for (int jj = 0; jj < NJ; ++jj) {
 #pragma unroll
       for (int c = 0; c < C; ++c) p[jj][c] = t.x[c][j0 + jj];
-      softmax_fast<C>(p[jj]);
+      softmax_fixed<C>(p[jj]);
       lab[jj] = fast_label<C>(t.lab[j0 + jj]);
 #pragma unroll
       for (int c = 0; c < C; ++c) g[jj][c] = bucket_guess(p[jj][c], nf);
@@ -1336,10 +1378,13 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
         for (int c = 0; c < C; ++c) {
           if (c == 0 && skip0) continue;
           const int k = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
-          const uint32_t q = fixq(p[jj][c]);
-          const uint32_t hi = (lab[jj] == (uint32_t)c)
-                                  ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
-                                  : (1u << (kShiftN - 32));
+          const uint32_t q = cvt_u32(p[jj][c]);
+          uint32_t hi;
+          if constexpr (C <= 4)
+            hi = packed_high(label_bytes(t.lab[j0 + jj], C), c);
+          else
+            hi = (lab[jj] == (uint32_t)c) ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
+                                          : (1u << (kShiftN - 32));
           lds_add(bin_at(hb[c], k, lsh), ((unsigned long long)hi << 32) | q);
         }
       } else {
@@ -1351,7 +1396,7 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
         for (int c = 0; c < C; ++c) {
           if (c == 0 && skip0) continue;
           const int h = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
-          const uint32_t q = fixq(p[jj][c]);
+          const uint32_t q = cvt_u32(p[jj][c]);
           // the square of the quantised p (q 2^-30), exact in 64 bits,
           // rounded to the same fixed point: the moments then describe one
           // set of values (a float32 p * p would carry a 2^-24 relative
@@ -1373,19 +1418,19 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
   }
 }
 
-template <typename T, int C, int VEC, bool SOFT, bool RIGHT>
+// SKIP0: channel 0 (background) is not in the loss (P.off == 1).
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
 __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* tabs = reinterpret_cast<float*>(smem);
   const int K = P.K;
   const int n = SOFT ? 2 * K : K;
-  const int off = P.off;
+  constexpr int off = SKIP0 ? 1 : 0;
   const int CL = C - off;
   const int CK = CL * K;
   const int R = P.copies;
   const int lr = __builtin_ctz((unsigned)R);
   const int lsh = lr + 3;
-  const bool skip0 = off != 0;
   const int tid = threadIdx.x;
   const int64_t blk = blockIdx.x;
   const int b = (int)(blk / P.tiles);
@@ -1438,7 +1483,7 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
     fast_load<T, C, VEC>(ta, px, pl, pipe ? at(0) : 0u, true);
     fast_load<T, C, VEC>(tb, px, pl, pipe ? at(1) : 0u, true);
   }
-  treg.store(tabs, P.btab, P.rtab, n, nrepl);
+  treg.store(tabs, P.btab, P.rtab, n, nrepl, 0x1p30f);
   {
     unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
     for (size_t i = tid; i < hist_words; i += kThreads) h64[i] = 0ull;
@@ -1457,24 +1502,24 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   if (nsteps > 0) {
     int i = 0;
     for (; i + 2 < nsteps; i += 2) {
-      fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, skip0, lsh, hb, words);
+      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, repl, K, lsh, hb, words);
       fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), true);
-      fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, skip0, lsh, hb, words);
+      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, repl, K, lsh, hb, words);
       fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), true);
     }
-    fast_accumulate<C, VEC, SOFT, RIGHT>(ta, tab, repl, K, skip0, lsh, hb, words);
-    if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT>(tb, tab, repl, K, skip0, lsh, hb, words);
+    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, repl, K, lsh, hb, words);
+    if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, repl, K, lsh, hb, words);
   }
   // remaining full vectors (not every thread has one), then single voxels
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
     fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, true);
-    fast_accumulate<C, VEC, SOFT, RIGHT>(t, tab, repl, K, skip0, lsh, hb, words);
+    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, repl, K, lsh, hb, words);
   }
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     FastTile<C, 1> t;
     fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, true);
-    fast_accumulate<C, 1, SOFT, RIGHT>(t, tab, repl, K, skip0, lsh, hb, words);
+    fast_accumulate<C, 1, SOFT, RIGHT, SKIP0>(t, tab, repl, K, lsh, hb, words);
   }
   __syncthreads();
   fwd_finish<SOFT, SOFT>(P, H, hist, repl, CK, CL, b, tile, true);
@@ -1505,10 +1550,11 @@ __device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const flo
 }
 
 // Backward of one tile, in place in t.x (logits in, gradient out).
-template <int C, int VEC, bool SOFT, bool RIGHT>
+template <int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
 __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* tab,
                                               const float* sab, const float* scoef,
-                                              const float* sg, int K, int off) {
+                                              const float* sg, int K) {
+  constexpr int off = SKIP0 ? 1 : 0;
   const float nf = (float)(SOFT ? 2 * K : K);
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
@@ -1542,13 +1588,13 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
   }
 }
 
-template <typename T, int C, int VEC, bool SOFT, bool RIGHT>
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
 __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* tabs = reinterpret_cast<float*>(smem);
   const int K = P.K;
   const int n = SOFT ? 2 * K : K;
-  const int off = P.off;
+  constexpr int off = SKIP0 ? 1 : 0;
   const int CL = C - off;
   const int CK = CL * K;
   const int tid = threadIdx.x;
@@ -1630,20 +1676,20 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   if (nsteps > 0) {
     int i = 0;
     for (; i + 2 < nsteps; i += 2) {
-      fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, sab, scoef, sg, K, off);
+      fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, sab, scoef, sg, K);
 #pragma unroll
       for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i), ta.x[c]);
       fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), SOFT);
-      fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, sab, scoef, sg, K, off);
+      fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, sab, scoef, sg, K);
 #pragma unroll
       for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i + 1), tb.x[c]);
       fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), SOFT);
     }
-    fast_backward<C, VEC, SOFT, RIGHT>(ta, tab, sab, scoef, sg, K, off);
+    fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, sab, scoef, sg, K);
 #pragma unroll
     for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i), ta.x[c]);
     if (i + 1 < nsteps) {
-      fast_backward<C, VEC, SOFT, RIGHT>(tb, tab, sab, scoef, sg, K, off);
+      fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, sab, scoef, sg, K);
 #pragma unroll
       for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i + 1), tb.x[c]);
     }
@@ -1651,14 +1697,14 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
     fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, SOFT);
-    fast_backward<C, VEC, SOFT, RIGHT>(t, tab, sab, scoef, sg, K, off);
+    fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, sab, scoef, sg, K);
 #pragma unroll
     for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + v, t.x[c]);
   }
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     FastTile<C, 1> t;
     fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, SOFT);
-    fast_backward<C, 1, SOFT, RIGHT>(t, tab, sab, scoef, sg, K, off);
+    fast_backward<C, 1, SOFT, RIGHT, SKIP0>(t, tab, sab, scoef, sg, K);
 #pragma unroll
     for (int c = 0; c < C; ++c) dr[c][v] = from_f32<T>(t.x[c][0]);
   }
@@ -1682,7 +1728,8 @@ hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) 
   auto kern = fwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
   if constexpr (has_fast<CMAX, EXACT>()) {
     if (prm.act == kActSoftmax && prm.tk == kTgtLabels)
-      kern = fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT>;
+      kern = prm.off ? fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true>
+                     : fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false>;
   }
   if (g.lds_fwd > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1700,7 +1747,8 @@ hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) 
   if constexpr (has_fast<CMAX, EXACT>()) {
     // the hard gradient reads no targets: any target layout takes the fast path
     if (prm.act == kActSoftmax && (!SOFT || prm.tk == kTgtLabels))
-      kern = bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT>;
+      kern = prm.off ? bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true>
+                     : bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false>;
   }
   if (g.lds_bwd > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

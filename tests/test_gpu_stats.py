@@ -75,13 +75,15 @@ def test_stats_exact_on_given_probabilities(binning, kind, right, num_bins, chan
         np.testing.assert_allclose(st[2], sg, rtol=0, atol=tol.max())
 
 
+@pytest.mark.parametrize("channels", [2, 3, 4, 5, 16])
 @pytest.mark.parametrize("include_background", [True, False])
 @pytest.mark.parametrize("binning", ["hard", "soft"])
-def test_stats_with_labels_and_softmax(binning, include_background) -> None:
-    """Index targets (fused one-hot) and in-kernel softmax; background dropped."""
+def test_stats_with_labels_and_softmax(binning, include_background, channels) -> None:
+    """Index targets (fused one-hot) and in-kernel softmax; background dropped.
+    C = 2, 3, 4, 16 run the fast kernels, C = 5 the generic one."""
     config = ACEConfig(binning=binning, to_onehot_y=True, include_background=include_background)
-    x, labels = _inputs("logits", 2, 5, (40, 40, 9), 5, 20)
-    say(f"stats labels {binning} bg={include_background}")
+    x, labels = _inputs("logits", 2, channels, (40, 40, 9), 5, 20)
+    say(f"stats labels {binning} bg={include_background} C={channels}")
     *_, st = hip_stats(x.cuda(), labels.cuda(), config)
     st = st.cpu().numpy()
     w, sp, sg = _truth(x, labels, config)
@@ -92,6 +94,9 @@ def test_stats_with_labels_and_softmax(binning, include_background) -> None:
         assert moved <= 4, moved
         assert st[0].sum() == w.sum()
         assert st[2].sum() == sg.sum()  # every labelled voxel counted once
+        # ... and for its own class: per-class label counts are exact
+        np.testing.assert_array_equal(st[2].sum(-1), sg.sum(-1))
+        assert np.abs(st[2] - sg).sum() <= moved
         np.testing.assert_allclose(st[1], sp, rtol=0, atol=1e-5 * max(1.0, np.abs(sp).max()))
     else:
         np.testing.assert_allclose(st[0].sum(-1), n, rtol=1e-6)  # weights sum to 1 per voxel
