@@ -1411,8 +1411,9 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
           ga = hit ? a : ga;
           gq = hit ? q : gq;
         }
-        if (lab[jj] != 0xffffffffu && !(lab[jj] == 0u && skip0))
-          lds_add(ga + 2 * words, (unsigned long long)gq);
+        // unconditional: without a labelled loss channel gq is 0 and ga the
+        // first half-bin of channel 0's copy, so the add changes nothing
+        lds_add(ga + 2 * words, (unsigned long long)gq);
       }
     }
   }
