@@ -509,6 +509,23 @@ __device__ __forceinline__ float wave_sum(float v) {
           __int_as_float(__builtin_amdgcn_readlane(b, 47))) +
          __int_as_float(__builtin_amdgcn_readlane(b, 63));
 }
+// Sum over the seg lanes (16, 32 or 64) of segment `sub` of a wave, every
+// lane active: the DPP row totals of wave_sum, added per segment in row
+// order (seg 64: exactly wave_sum's order).
+__device__ __forceinline__ float seg_sum(float v, int sub, int seg) {
+  v += __int_as_float(row_shr<1>(__float_as_int(v)));
+  v += __int_as_float(row_shr<2>(__float_as_int(v)));
+  v += __int_as_float(row_shr<4>(__float_as_int(v)));
+  v += __int_as_float(row_shr<8>(__float_as_int(v)));
+  const int b = __float_as_int(v);
+  const float t0 = __int_as_float(__builtin_amdgcn_readlane(b, 15));
+  const float t1 = __int_as_float(__builtin_amdgcn_readlane(b, 31));
+  const float t2 = __int_as_float(__builtin_amdgcn_readlane(b, 47));
+  const float t3 = __int_as_float(__builtin_amdgcn_readlane(b, 63));
+  if (seg == 64) return ((t0 + t1) + t2) + t3;
+  if (seg == 32) return sub == 0 ? t0 + t1 : t2 + t3;
+  return sub == 0 ? t0 : (sub == 1 ? t1 : (sub == 2 ? t2 : t3));
+}
 __device__ __forceinline__ int wave_sum(int v) {
   v += row_shr<1>(v);
   v += row_shr<2>(v);
@@ -662,40 +679,67 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
     P.d[o] = dd;
   }
   __syncthreads();
-  // one wave per class row
+  // class rows: K <= 64 bins per row take one lane each, 64 / seg rows per
+  // wave (seg = 16, 32 or 64 lanes per row); longer rows loop over a wave
   const int lane = tid & 63;
   const int rows = P.B * CL;
-  for (int row = tid >> 6; row < nb * CL; row += kThreads / 64) {
-    const int base = row * K;  // == bb * CK + cl * K
+  const int nrows = nb * CL;
+  auto row_tail = [&](int row, float fcls, float present) {
     const int bb = nb == 1 ? 0 : row / CL;
     const int cl = row - bb * CL;
-    const int64_t ob = (int64_t)(b0 + bb) * CK + cl * K;
-    int kne;
-    float fcls, present;
-    if (K <= 64) {
+    const float w = P.clsw ? P.clsw[cl] : 1.0f;
+    float fw = P.ignore_empty ? fcls * present : fcls;
+    fw = fw * w;
+    float jac = P.ignore_empty ? present * w : w;
+    if (P.red == kRedMean) jac = jac / (float)rows;
+    const int gi = (b0 + bb) * CL + cl;
+    P.f[gi] = fw;
+    sf[row] = fw;
+    P.jac[gi] = jac;
+  };
+  if (K <= 64) {
+    const int seg = K <= 16 ? 16 : (K <= 32 ? 32 : 64);
+    const int per_wave = 64 / seg;
+    const int sub = lane / seg;
+    const int kl = lane & (seg - 1);
+    const unsigned long long smask = (seg == 64 ? ~0ull : ((1ull << seg) - 1)) << (sub * seg);
+    for (int r0 = (tid >> 6) * per_wave; r0 < nrows; r0 += (kThreads / 64) * per_wave) {
+      const int row = r0 + sub;
+      const bool rv = row < nrows;
+      const bool in = rv && kl < K;
+      const int rr = rv ? row : r0;  // an in-range row for idle lanes
       // one bin per lane: every LDS value read once, in one round trip
-      const bool in = lane < K;
-      const int i = base + (in ? lane : 0);
+      const int i = rr * K + (in ? kl : 0);
       const float dd = sd[i];
       const float wv = sw[i];
       const float gv = sg[i];
       const bool emp = se[i] != 0;
       const bool ne = in && !emp;
-      kne = __popcll(__ballot(ne));
-      const float err = wave_sum(ne ? fabsf(dd) : 0.0f);
-      const float gsum = wave_sum(in ? gv : 0.0f);
+      const int kne = __popcll(__ballot(ne) & smask);
+      const float err = seg_sum(ne ? fabsf(dd) : 0.0f, sub, seg);
+      const float gsum = seg_sum(in ? gv : 0.0f, sub, seg);
       // the row's serial tail: v_rcp_f32 (1 ulp) instead of IEEE quotients
       // for f = mean |d| and coef = sign(d) / (K_ne W), far inside the loss
       // and gradient tolerances
-      fcls = kne > 0 ? err * __builtin_amdgcn_rcpf((float)kne) : __builtin_nanf("");
-      present = gsum > 0.0f ? 1.0f : 0.0f;
+      const float fcls = kne > 0 ? err * __builtin_amdgcn_rcpf((float)kne) : __builtin_nanf("");
+      const float present = gsum > 0.0f ? 1.0f : 0.0f;
       const float kf = (float)(kne > 0 ? kne : 1);
       if (in) {
+        const int bb = nb == 1 ? 0 : rr / CL;
+        const int cl = rr - bb * CL;
+        const int64_t ob = (int64_t)(b0 + bb) * CK + cl * K;
         const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
-        P.coef[ob + lane] = emp ? 0.0f : sgn * __builtin_amdgcn_rcpf(kf * wv);
+        P.coef[ob + kl] = emp ? 0.0f : sgn * __builtin_amdgcn_rcpf(kf * wv);
       }
-    } else {
-      kne = 0;
+      if (rv && kl == 0) row_tail(row, fcls, present);
+    }
+  } else {
+    for (int row = tid >> 6; row < nrows; row += kThreads / 64) {
+      const int base = row * K;  // == bb * CK + cl * K
+      const int bb = nb == 1 ? 0 : row / CL;
+      const int cl = row - bb * CL;
+      const int64_t ob = (int64_t)(b0 + bb) * CK + cl * K;
+      int kne = 0;
       float err = 0.0f, gsum = 0.0f;
       for (int k = lane; k < K; k += 64) {
         if (!se[base + k]) {
@@ -707,25 +751,15 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
       kne = wave_sum(kne);
       err = wave_sum(err);
       gsum = wave_sum(gsum);
-      fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
-      present = gsum > 0.0f ? 1.0f : 0.0f;
+      const float fcls = kne > 0 ? err / (float)kne : __builtin_nanf("");
+      const float present = gsum > 0.0f ? 1.0f : 0.0f;
       const float kf = (float)(kne > 0 ? kne : 1);
       for (int k = lane; k < K; k += 64) {
         const float dd = sd[base + k];
         const float sgn = dd > 0.0f ? 1.0f : (dd < 0.0f ? -1.0f : 0.0f);
         P.coef[ob + k] = se[base + k] ? 0.0f : sgn / (kf * sw[base + k]);
       }
-    }
-    if (lane == 0) {
-      const float w = P.clsw ? P.clsw[cl] : 1.0f;
-      float fw = P.ignore_empty ? fcls * present : fcls;
-      fw = fw * w;
-      float jac = P.ignore_empty ? present * w : w;
-      if (P.red == kRedMean) jac = jac / (float)rows;
-      const int gi = (b0 + bb) * CL + cl;
-      P.f[gi] = fw;
-      sf[row] = fw;
-      P.jac[gi] = jac;
+      if (lane == 0) row_tail(row, fcls, present);
     }
   }
   float total = 0.0f;

@@ -130,7 +130,12 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   int steps = steps_override;
   if (steps <= 0) {
     const int64_t total = B * (N > 0 ? N : 1);
-    const int64_t target_blocks = 1024;
+    // ~4 blocks per CU; half that above 8 channels, whose kernels hold ~120
+    // VGPRs (4 waves per SIMD: 1024 blocks would just fill the chip, and
+    // on MI355X ~10% of them started a round late) and issue C x K x 3
+    // final-sum atomics per block (cfg 4, C = 16: 52 us at 512 blocks vs
+    // 57 us at 1024)
+    const int64_t target_blocks = C > 8 ? 512 : 1024;
     steps = (int)cdiv(total, step_vox * target_blocks);
     if (steps < 1) steps = 1;
     if (steps > 64) steps = 64;
