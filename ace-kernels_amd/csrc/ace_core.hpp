@@ -565,6 +565,37 @@ __device__ __forceinline__ void moment_terms(double n, double g, double s1, doub
   out[5] = (sg - cl * g) * inv;
 }
 
+// Sums over the `reps` replicas of NVAL final-sum words of one item (word j
+// at fb + r * NV + j * stride + idx).  Every load is unconditional -- the
+// replica index is clamped to reps - 1 and the extra replicas are dropped
+// after loading -- so all of them are in flight at once and a caller can
+// issue a second item's loads before it waits for the first's.
+template <int NVAL>
+__device__ __forceinline__ void load_sums(const unsigned long long* fb, int NV, int reps, int stride,
+                                          int idx, long long (&out)[NVAL]) {
+  unsigned long long v[kMaxReps][NVAL];
+#pragma unroll
+  for (int r = 0; r < kMaxReps; ++r) {
+    const int rr = r < reps ? r : reps - 1;
+#pragma unroll
+    for (int j = 0; j < NVAL; ++j) v[r][j] = load_dev(fb + (int64_t)rr * NV + j * stride + idx);
+  }
+#pragma unroll
+  for (int j = 0; j < NVAL; ++j) {
+    long long acc = 0;
+#pragma unroll
+    for (int r = 0; r < kMaxReps; ++r)
+      if (r < reps) acc += (long long)v[r][j];
+    out[j] = acc;
+  }
+}
+template <int NVAL>
+__device__ __forceinline__ void zero_sums(unsigned long long* fb, int NV, int reps, int stride, int idx) {
+  for (int r = 0; r < reps; ++r)
+#pragma unroll
+    for (int j = 0; j < NVAL; ++j) store_dev(fb + (int64_t)r * NV + j * stride + idx, 0ull);
+}
+
 // Epilogue of batch indices [b0, b0 + nb) in one block.  Final sums -> W, P,
 // G per bin, d = P/W - G/W (kernels/epilogue.py:23-82); per class row: K_ne,
 // f, coef, jac (one wave per row).  It leaves its final sums zero and returns
@@ -604,18 +635,18 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
           for (int v = 0; v < 5; ++v) m[v] += (long long)load_dev(&f[v * H2 + th]);
         }
       }
-      for (int r = 0; r < reps; ++r) {
-        unsigned long long* f = fb + (int64_t)r * NV;
-#pragma unroll
-        for (int v = 0; v < 5; ++v) store_dev(&f[v * H2 + th], 0ull);
-      }
+      zero_sums<5>(fb, NV, reps, H2, th);
       const int hh = th % (2 * K);
       moment_terms((double)m[0], (double)m[1], (double)m[2] * dscale, (double)m[3] * dscale,
                    (double)m[4] * dscale, (double)repl[hh], (double)repl[hh + 2], terms + 6 * t);
     }
     __syncthreads();
   }
-  for (int i = tid; i < NB; i += kThreads) {
+  // per bin: W, P, G (final sums, or the half-bin terms of soft moments),
+  // then d; without moments two bins per thread and pass, both bins' loads
+  // in flight together
+  auto fb_of = [&](int i) { return P.fin + (int64_t)(b0 + (nb == 1 ? 0 : i / CK)) * reps * NV; };
+  auto bin = [&](int i, const long long (&sm)[3]) {
     const int bb = nb == 1 ? 0 : i / CK;
     const int t = i - bb * CK;
     double Wd, Pd, Gd;
@@ -639,27 +670,10 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
         }
       }
     } else {
-      // every replica's three sums in flight at once (reps <= kMaxReps)
-      unsigned long long* fb = P.fin + (int64_t)(b0 + bb) * reps * NV;
-      long long s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-      for (int r = 0; r < kMaxReps; ++r) {
-        if (r < reps) {
-          unsigned long long* f = fb + (int64_t)r * NV;
-          s0 += (long long)load_dev(&f[t]);
-          s1 += (long long)load_dev(&f[CK + t]);
-          s2 += (long long)load_dev(&f[2 * CK + t]);
-        }
-      }
-      for (int r = 0; r < reps; ++r) {
-        unsigned long long* f = fb + (int64_t)r * NV;
-        store_dev(&f[t], 0ull);
-        store_dev(&f[CK + t], 0ull);
-        store_dev(&f[2 * CK + t], 0ull);
-      }
-      Wd = (double)s0 * dscale;
-      Pd = (double)s1 * dscale;
-      Gd = (double)s2 * dscale;
+      zero_sums<3>(fb_of(i), NV, reps, CK, t);
+      Wd = (double)sm[0] * dscale;
+      Pd = (double)sm[1] * dscale;
+      Gd = (double)sm[2] * dscale;
     }
     const int64_t o = (int64_t)(b0 + bb) * CK + t;
     if (P.stats) {
@@ -677,6 +691,19 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
     sg[i] = Gf;
     se[i] = empty ? 1 : 0;
     P.d[o] = dd;
+  };
+  if constexpr (MOM) {
+    const long long none[3] = {0, 0, 0};
+    for (int i = tid; i < NB; i += kThreads) bin(i, none);
+  } else {
+    for (int i0 = tid; i0 < NB; i0 += 2 * kThreads) {
+      const int i1 = i0 + kThreads < NB ? i0 + kThreads : i0;
+      long long s0[3], s1[3];
+      load_sums<3>(fb_of(i0), NV, reps, CK, i0 - (nb == 1 ? 0 : i0 / CK) * CK, s0);
+      load_sums<3>(fb_of(i1), NV, reps, CK, i1 - (nb == 1 ? 0 : i1 / CK) * CK, s1);
+      bin(i0, s0);
+      if (i1 != i0) bin(i1, s1);
+    }
   }
   __syncthreads();
   // class rows: K <= 64 bins per row take one lane each, 64 / seg rows per
@@ -1382,7 +1409,9 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
   // nothing.  C = 16: one voxel at a time, each table read just before its
   // use (the batched form would need more than 128 registers).
   constexpr bool BATCH = C <= 4;
-  constexpr int NJ = BATCH ? VEC : 1;
+  // soft: two voxels at a time (four would hold 111 VGPRs at C = 4, leaving
+  // exactly the 4 waves per SIMD the 1024 blocks need)
+  constexpr int NJ = BATCH ? (SOFT && VEC > 2 ? 2 : VEC) : 1;
 #pragma unroll
   for (int j0 = 0; j0 < VEC; j0 += NJ) {
     float p[NJ][C];
