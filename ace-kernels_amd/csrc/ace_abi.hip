@@ -179,7 +179,8 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
   const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
   // soft + softmax + labels on a fast channel count: the moments kernels
-  const bool moments = soft && labels && act == kActSoftmax && fast_channels(channels);
+  const bool moments = soft && labels && act == kActSoftmax && fast_channels(channels) &&
+                       num_bins <= kMomentMaxBins;
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
                                    include_background != 0, labels, env_steps("ACE_FWD_STEPS"),
                                    env_copies(), moments);
@@ -211,6 +212,13 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   p.ignore_empty = ignore_empty_classes != 0;
   p.red = reduction;
   p.empty_w = empty_weight;
+  if (moments) {
+    const MomentScale ms = moment_scale(num_bins);
+    p.msc = ldexpf(1.0f, ms.m);
+    p.misc = ldexpf(1.0f, -ms.m);
+    p.mw = ms.w;
+    p.mshift = moment_shift(voxels);
+  }
   p.btab = bin_table;
   p.rtab = centre_table;
   p.clsw = class_weight;
@@ -245,7 +253,8 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   if (soft && !diff) return ACE_EINVAL;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
   const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
-  const bool moments = soft && labels && act == kActSoftmax && fast_channels(channels);
+  const bool moments = soft && labels && act == kActSoftmax && fast_channels(channels) &&
+                       num_bins <= kMomentMaxBins;
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
                                    include_background != 0, labels, env_steps("ACE_BWD_STEPS"), 0,
                                    moments);

@@ -83,4 +83,44 @@ ACE_HD int bucket_unit(float p, float nf, const float* tab) {
   return bucket_fix<RIGHT>(g, tab[g + 1], p);
 }
 
+// Fixed point of the soft moments (per half-bin sums of p and p^2).  A
+// probability in half-bin h is quantised to q = trunc(p 2^m) and stored as
+// its offset u = q - h w from the integer base h w, so that u^2 is exact in
+// 64 bits and the sums describe the quantised values exactly (the moment
+// formulas subtract nearly equal sums, so a rounded p^2 would carry its
+// rounding, amplified by 1 / S = 2K, into P).  q is exact (p 2^m is an
+// integer) for p >= 2^(23-m): p >= 2^-5 at m = 28 (K = 16..31).  With the half boundaries e_h = h / 2K (1 + d_h), |d_h| < 8 2^-24
+// (see bucket_unit), and ws = 2^m / 2K <= 2^23:
+//   w <= ws (1 - 2^-14) and h w < e_h 2^m for h >= 1, so u >= 0;
+//   u <= e_{h+1} 2^m - h w < ws (1 + 2K (2^-14 + 2^-21)) + 2K
+//     < 1.26 * 2^23 + 2^12 < 2^24 = kMomentUMax for 2K <= 2^12,
+// so h w and u^2 are 24-bit multiplies (w < 2^23 fits a signed one).
+// m = 23 + floor(log2 2K) (ws > 2^22), at most 30.
+constexpr int kMomentMaxBins = 2048;
+constexpr unsigned kMomentUMax = 1u << 24;
+
+struct MomentScale {
+  int m;  // q = trunc(p 2^m)
+  int w;  // base of half-bin h: h w
+};
+
+ACE_HD MomentScale moment_scale(int num_bins) {
+  int lg = 0;
+  while ((2ll << lg) <= 2ll * num_bins) ++lg;  // floor(log2 2K)
+  MomentScale s;
+  s.m = 23 + lg < 30 ? 23 + lg : 30;
+  const double ws = (double)(1ll << s.m) / (2.0 * num_bins);
+  s.w = (int)(ws * (1.0 - 1.0 / 16384.0));
+  return s;
+}
+
+// Right shift of the per-copy sums of u^2 before they are added into the
+// final sums of a batch index of N voxels: u^2 < 2^48, one copy holds at
+// most 2047 voxels (< 2^59), and N 2^48 / 2^shift < 2^62.
+ACE_HD int moment_shift(long long voxels) {
+  int bits = 0;
+  while (bits < 62 && (1ll << bits) <= voxels) ++bits;  // bit length of N
+  return bits > 14 ? bits - 14 : 0;
+}
+
 }  // namespace ace

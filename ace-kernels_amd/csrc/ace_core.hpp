@@ -59,6 +59,10 @@ struct FwdParams {
   int lchunk;          // log2 of the copies one lane adds before unpacking
   int epi_all;         // one block runs every batch index's epilogue and the loss
   float empty_w;
+  float msc;           // soft moments: 2^m, the fixed-point scale of p (moment_scale)
+  float misc;          // 2^-m
+  int mw;              // soft moments: half-bin h has base h mw (in units of 2^-m)
+  int mshift;          // soft moments: right shift of the per-copy sums of u^2
   const float* btab;   // bucket table (K or 2K upper boundaries)
   const float* rtab;   // soft centre table (2K + 2)
   const float* clsw;   // C' class weights or null
@@ -72,6 +76,14 @@ struct FwdParams {
   float* f;
   float* loss;
   double* stats;
+};
+
+// Soft moments fixed point in the main loop: p scaled by sc = 2^m (isc =
+// 2^-m); nw = -w (the half-bin base is h w).
+struct MomentScaleArgs {
+  float sc;
+  float isc;
+  int nw;
 };
 
 struct BwdParams {
@@ -190,6 +202,21 @@ __device__ __forceinline__ float rcp_rn(float b) {
 // div_rn(a, b, y): ace_bins.hpp (shared with the CPU test harness).
 
 // A probability already scaled by 2^30 (p in [0, 2^30] or NaN) as 30-bit
+// a * b + c with 24-bit signed a, b (v_mad_i32_i24; the compiler would
+// otherwise sign-extend a it cannot bound first).
+__device__ __forceinline__ uint32_t mad_i24(int a, int b, uint32_t c) {
+  uint32_t r;
+  asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// u^2 for u < 2^24 as two 24-bit multiplies (low 32 and high 16 bits).
+__device__ __forceinline__ unsigned long long square_u24(uint32_t u) {
+  uint32_t lo, hi;
+  asm("v_mul_u32_u24 %0, %1, %1" : "=v"(lo) : "v"(u));
+  asm("v_mul_hi_u32_u24 %0, %1, %1" : "=v"(hi) : "v"(u));
+  return ((unsigned long long)hi << 32) | lo;
+}
+
 // fixed point, truncated: v_cvt_u32_f32 rounds toward zero and maps NaN to
 // 0.  At most 2^-30 below p.
 __device__ __forceinline__ uint32_t cvt_u32(float p30) {
@@ -546,23 +573,31 @@ __device__ __forceinline__ int* counter(const FwdParams& P, int64_t i) {
 // Soft moments: the bin sums of half-bin h (interval of half boundaries
 // between the replicated centres cl = repl[h] and cr = repl[h + 2]) follow
 // from its moments, because both interpolation weights are linear in p there:
-// lw = (cr - p) / S, rw = (p - cl) / S with S = cr - cl (common.py:43-61), so
-//   W_l += (cr n - S1) / S,   W_r += (S1 - cl n) / S,
-//   P_l += (cr S1 - S2) / S,  P_r += (S2 - cl S1) / S,
-//   G_l += (cr g - Sg) / S,   G_r += (Sg - cl g) / S
-// with n = count, S1 = sum p, S2 = sum p^2, g = labelled count, Sg = sum p
-// over the labelled voxels; bins l = max(h-1,0)/2, r = min(h+1,2K-1)/2.  The
-// weights are the exact-arithmetic ones (the reference rounds ld, rd and S to
-// float32 per voxel: a ~1e-7 relative difference per voxel).
-__device__ __forceinline__ void moment_terms(double n, double g, double s1, double s2, double sg,
-                                             double cl, double cr, double* out) {
+// lw = (cr - p) / S, rw = (p - cl) / S with S = cr - cl (common.py:43-61).
+// The kernels store each p of half-bin h as L + v, L its base and v its
+// offset (moment_scale: p quantised to 2^-m, v = u 2^-m), so with
+// a = cr - L, b = L - cl (a + b = S), V1 = sum v, V2 = sum v^2, Vg = sum v
+// over the labelled voxels, n = count and g = labelled count:
+//   W_l += (n a - V1) / S,               W_r += (n b + V1) / S,
+//   P_l += (n a L + (a - L) V1 - V2) / S, P_r += (n b L + (b + L) V1 + V2) / S,
+//   G_l += (g a - Vg) / S,               G_r += (g b + Vg) / S;
+// bins l = max(h-1,0)/2, r = min(h+1,2K-1)/2.  The sums are exact for the
+// quantised p, and W, P and G describe the same values, so d = P/W - G/W
+// keeps its precision in bins of one or two voxels with small weights
+// (P_l cancels to p (cr - p) there).  The weights are the exact-arithmetic
+// ones (the reference rounds ld, rd and S to float32 per voxel: a ~1e-7
+// relative difference per voxel).
+__device__ __forceinline__ void moment_terms(double n, double g, double v1, double v2, double vg,
+                                             double L, double cl, double cr, double* out) {
   const double inv = 1.0 / (cr - cl);
-  out[0] = (cr * n - s1) * inv;
-  out[1] = (s1 - cl * n) * inv;
-  out[2] = (cr * s1 - s2) * inv;
-  out[3] = (s2 - cl * s1) * inv;
-  out[4] = (cr * g - sg) * inv;
-  out[5] = (sg - cl * g) * inv;
+  const double a = cr - L;
+  const double b = L - cl;
+  out[0] = (n * a - v1) * inv;
+  out[1] = (n * b + v1) * inv;
+  out[2] = (n * a * L + (a - L) * v1 - v2) * inv;
+  out[3] = (n * b * L + (b + L) * v1 + v2) * inv;
+  out[4] = (g * a - vg) * inv;
+  out[5] = (g * b + vg) * inv;
 }
 
 // Sums over the `reps` replicas of NVAL final-sum words of one item (word j
@@ -618,6 +653,7 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
   double* terms = reinterpret_cast<double*>(hist + L.terms);  // [nb * 2CK][6]
   const int64_t BCK = (int64_t)P.B * CK;
   const double dscale = 1.0 / 1073741824.0;
+  const double mscale = (double)P.misc;
   if constexpr (MOM) {
     // per half-bin: the five moments (every replica in flight at once), then
     // its six contributions
@@ -637,8 +673,10 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
       }
       zero_sums<5>(fb, NV, reps, H2, th);
       const int hh = th % (2 * K);
-      moment_terms((double)m[0], (double)m[1], (double)m[2] * dscale, (double)m[3] * dscale,
-                   (double)m[4] * dscale, (double)repl[hh], (double)repl[hh + 2], terms + 6 * t);
+      const double L = (double)((long long)hh * P.mw) * mscale;
+      moment_terms((double)m[0], (double)m[1], (double)m[2] * mscale,
+                   (double)m[3] * (mscale * mscale * (double)(1ll << P.mshift)),
+                   (double)m[4] * mscale, L, (double)repl[hh], (double)repl[hh + 2], terms + 6 * t);
     }
     __syncthreads();
   }
@@ -859,8 +897,29 @@ __device__ __forceinline__ long long sum_copies(const T* a, int w0, int s) {
   return acc;
 }
 
-// Moments variant: 5 values per half-bin (count, labelled count, sum p,
-// sum p^2, labelled sum p; counts unscaled), fin layout [5][2CK].
+// Sum of the R copies, each rounded to a multiple of 2^sh first (the sums
+// of u^2: one copy is below 2^59, a batch index's total after the shift
+// below 2^62 -- moment_shift).
+template <int R, int BATCH = kSumBatch>
+__device__ __forceinline__ long long sum_copies_shifted(const unsigned long long* a, int w0, int s,
+                                                        int sh) {
+  constexpr int NB = R < BATCH ? R : BATCH;
+  const unsigned long long half = sh > 0 ? 1ull << (sh - 1) : 0ull;
+  long long acc = 0;
+#pragma unroll 1
+  for (int r0 = 0; r0 < R; r0 += NB) {
+    unsigned long long v[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) v[j] = a[w0 + ((r0 + j + s) & (R - 1))];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc += (long long)((v[j] + half) >> sh);
+  }
+  return acc;
+}
+
+// Moments variant: 5 values per half-bin (count, labelled count, sum u,
+// sum u^2 >> mshift, labelled sum u of the offsets u of moment_scale;
+// counts unscaled), fin layout [5][2CK].
 template <int R>
 __device__ __forceinline__ void block_moments_r(const FwdParams& P, const Hist& H, int CK,
                                                 unsigned long long* fin) {
@@ -870,7 +929,7 @@ __device__ __forceinline__ void block_moments_r(const FwdParams& P, const Hist& 
     long long m[5] = {0, 0, 0, 0, 0};
     // three arrays: half batches keep the registers of the main loop's
     sum_packed<R, kSumBatch / 2>(H.a, t * R, t, chunk, m[0], m[1], m[2]);
-    m[3] = sum_copies<R, kSumBatch / 2>(H.m2, t * R, t);
+    m[3] = sum_copies_shifted<R, kSumBatch / 2>(H.m2, t * R, t, P.mshift);
     m[4] = sum_copies<R, kSumBatch / 2>(H.mg, t * R, t);
 #pragma unroll
     for (int v = 0; v < 5; ++v)
@@ -1352,14 +1411,14 @@ __device__ __forceinline__ void softmax_fast(float (&x)[C]) {
   for (int c = 0; c < C; ++c) x[c] = div_rn(x[c], s, y);
 }
 
-// softmax_fast with every probability scaled by 2^30 (the fixed-point scale
-// of the histograms): q = e y 2^30, r = e - (s 2^-30) q, p = q + r y 2^30 are
-// the steps of div_rn with both factors scaled by powers of two, so p is
-// exactly 2^30 times the correctly rounded quotient (tiny quotients below
-// 2^-126 aside, which are bin 0 and 0 in fixed point either way) and one
-// multiply per channel is saved.
+// softmax_fast with every probability scaled by sc = 2^m (the fixed-point
+// scale of the histograms, isc = 2^-m): q = e y sc, r = e - (s isc) q,
+// p = q + r y sc are the steps of div_rn with both factors scaled by powers
+// of two, so p is exactly 2^m times the correctly rounded quotient (tiny
+// quotients below 2^-126 aside, which are bin 0 and 0 in fixed point either
+// way) and one multiply per channel is saved.
 template <int C>
-__device__ __forceinline__ void softmax_fixed(float (&x)[C]) {
+__device__ __forceinline__ void softmax_fixed(float (&x)[C], float sc, float isc) {
   const float m = max_of<C>(x);
   x[0] = exp_neg(x[0] - m);
   float s = x[0];
@@ -1368,8 +1427,8 @@ __device__ __forceinline__ void softmax_fixed(float (&x)[C]) {
     x[c] = exp_neg(x[c] - m);
     s += x[c];
   }
-  const float y = rcp_rn(s) * 0x1p30f;
-  const float s30 = s * 0x1p-30f;
+  const float y = rcp_rn(s) * sc;
+  const float s30 = s * isc;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const float q = x[c] * y;
@@ -1396,11 +1455,14 @@ __device__ __forceinline__ uint32_t packed_high(uint32_t X, int c) {
 // (background) is not in the loss.
 template <int C, int VEC, bool SOFT, bool RIGHT, bool skip0>
 __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const float* tab,
-                                                const float* repl, int K, int lsh,
+                                                const MomentScaleArgs& ms, int K, int lsh,
                                                 unsigned long long* const (&hb)[C],
                                                 const size_t words) {
-  // probabilities come scaled by 2^30 (softmax_fixed), the bucket table too
-  const float nf = (float)(SOFT ? 2 * K : K) * 0x1p-30f;
+  // probabilities come scaled by 2^30 (hard) or 2^m (soft moments) from
+  // softmax_fixed, the bucket table too
+  const float sc = SOFT ? ms.sc : 0x1p30f;
+  const float isc = SOFT ? ms.isc : 0x1p-30f;
+  const float nf = (float)(SOFT ? 2 * K : K) * isc;
   // C <= 4: all VEC voxels at a time -- every bin guess first, then every
   // table read, then the corrections and atomics.  The table reads cannot
   // move past an LDS atomic (same LDS array), so this order keeps VEC * C
@@ -1422,7 +1484,7 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
     for (int jj = 0; jj < NJ; ++jj) {
 #pragma unroll
       for (int c = 0; c < C; ++c) p[jj][c] = t.x[c][j0 + jj];
-      softmax_fixed<C>(p[jj]);
+      softmax_fixed<C>(p[jj], sc, isc);
       lab[jj] = fast_label<C>(t.lab[j0 + jj]);
 #pragma unroll
       for (int c = 0; c < C; ++c) g[jj][c] = bucket_guess(p[jj][c], nf);
@@ -1452,27 +1514,24 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
         }
       } else {
         // soft: moments of the voxel's half-bin h (count | labelled count |
-        // sum p packed as in hard binning, sum p^2, labelled sum p)
+        // sum u packed as in hard binning, sum u^2, labelled sum u) of the
+        // offset u = trunc(p 2^m) - h w < 2^24 from the half-bin's base
+        // (moment_scale): one 24-bit multiply-add, u^2 two 24-bit multiplies
         unsigned long long* ga = hb[0];
         uint32_t gq = 0u;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
           if (c == 0 && skip0) continue;
           const int h = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
-          const uint32_t q = cvt_u32(p[jj][c]);
-          // the square of the quantised p (q 2^-30), exact in 64 bits,
-          // rounded to the same fixed point: the moments then describe one
-          // set of values (a float32 p * p would carry a 2^-24 relative
-          // error that the moment formulas amplify by 1 / S)
-          const uint32_t q2 = (uint32_t)(((unsigned long long)q * q + (1ull << 29)) >> 30);
+          const uint32_t u = mad_i24(h, ms.nw, cvt_u32(p[jj][c]));
           const bool hit = lab[jj] == (uint32_t)c;
           const uint32_t hi = hit ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
                                   : (1u << (kShiftN - 32));
           unsigned long long* a = bin_at(hb[c], h, lsh);
-          lds_add(a, ((unsigned long long)hi << 32) | q);
-          lds_add(a + words, (unsigned long long)q2);
+          lds_add(a, ((unsigned long long)hi << 32) | u);
+          lds_add(a + words, square_u24(u));
           ga = hit ? a : ga;
-          gq = hit ? q : gq;
+          gq = hit ? u : gq;
         }
         // unconditional: without a labelled loss channel gq is 0 and ga the
         // first half-bin of channel 0's copy, so the add changes nothing
@@ -1547,7 +1606,8 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
     fast_load<T, C, VEC>(ta, px, pl, pipe ? at(0) : 0u, true);
     fast_load<T, C, VEC>(tb, px, pl, pipe ? at(1) : 0u, true);
   }
-  treg.store(tabs, P.btab, P.rtab, n, nrepl, 0x1p30f);
+  const MomentScaleArgs ms{P.msc, P.misc, -P.mw};
+  treg.store(tabs, P.btab, P.rtab, n, nrepl, SOFT ? ms.sc : 0x1p30f);
   {
     unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
     for (size_t i = tid; i < hist_words; i += kThreads) h64[i] = 0ull;
@@ -1566,24 +1626,24 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   if (nsteps > 0) {
     int i = 0;
     for (; i + 2 < nsteps; i += 2) {
-      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, repl, K, lsh, hb, words);
+      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, ms, K, lsh, hb, words);
       fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), true);
-      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, repl, K, lsh, hb, words);
+      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, ms, K, lsh, hb, words);
       fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), true);
     }
-    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, repl, K, lsh, hb, words);
-    if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, repl, K, lsh, hb, words);
+    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, ms, K, lsh, hb, words);
+    if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, ms, K, lsh, hb, words);
   }
   // remaining full vectors (not every thread has one), then single voxels
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
     fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, true);
-    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, repl, K, lsh, hb, words);
+    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, ms, K, lsh, hb, words);
   }
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     FastTile<C, 1> t;
     fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, true);
-    fast_accumulate<C, 1, SOFT, RIGHT, SKIP0>(t, tab, repl, K, lsh, hb, words);
+    fast_accumulate<C, 1, SOFT, RIGHT, SKIP0>(t, tab, ms, K, lsh, hb, words);
   }
   __syncthreads();
   fwd_finish<SOFT, SOFT>(P, H, hist, repl, CK, CL, b, tile, true);

@@ -194,6 +194,60 @@ long long check_near_edges_uncorrected(const float* table, int n, int right, int
   return bad;
 }
 
+// Soft moments fixed point (ace::moment_scale): for the 2K half boundaries
+// `table` (torch.linspace(0, 1 + eps, 2K + 1)[1:]) every half-bin's
+// smallest and largest quantised probability q = trunc(p 2^m) lies in
+// [h w, h w + 2^24), w < 2^23 and h w fits 32 bits.  p ranges over
+// (e_{h-1}, e_h] (right: [e_{h-1}, e_h)) with e_{-1} = 0 and p <= 1.
+// planted 1: m one larger; planted 2: w = ceil(ws) (no margin below the
+// boundaries).  Returns the violations.
+long long check_moment_offsets(const float* table, int K, int planted) {
+  ace::MomentScale s = ace::moment_scale(K);
+  if (planted == 1) {
+    s.m += 1;
+    s.w = (int)((double)(1ll << s.m) / (2.0 * K) * (1.0 - 1.0 / 16384.0));
+  } else if (planted == 2) {
+    s.w = (int)std::ceil((double)(1ll << s.m) / (2.0 * K));
+  }
+  const int n = 2 * K;
+  long long bad = s.w >= (1 << 23) ? 1 : 0;
+  const float sc = std::ldexp(1.0f, s.m);
+  for (int h = 0; h < n; ++h) {
+    const uint32_t qlo = h == 0 ? 0u : (uint32_t)(table[h - 1] * sc);
+    const uint32_t qhi = (uint32_t)(std::fmin(table[h], 1.0f) * sc);
+    const long long base = (long long)h * s.w;
+    if (base > 0x7fffffffLL) ++bad;
+    if ((long long)qlo < base) ++bad;
+    if ((long long)qhi - base >= (long long)ace::kMomentUMax) ++bad;
+  }
+  return bad;
+}
+
+// The offsets of every float32 p in [0, 1] (the softmax path: bucket_unit
+// half-bin h): 0 <= u < 2^24, and base + u reproduces q = trunc(p 2^m),
+// which equals p 2^m for p >= 2^(23 - m).  Returns the violations.
+long long check_moment_all(const float* table, int K, int right) {
+  const ace::MomentScale s = ace::moment_scale(K);
+  const int n = 2 * K;
+  const std::vector<float> tab = padded(table, n);
+  const float sc = std::ldexp(1.0f, s.m);
+  const float exact_from = std::ldexp(1.0f, 23 - s.m);
+  long long bad = 0;
+  const uint32_t z = to_bits(1.0f);
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+  for (int64_t b = 0; b <= (int64_t)z; ++b) {
+    const float p = from_bits((uint32_t)b);
+    const int h = right ? ace::bucket_unit<true>(p, (float)n, tab.data())
+                        : ace::bucket_unit<false>(p, (float)n, tab.data());
+    const float ps = p * sc;
+    const int64_t q = (int64_t)ps;
+    const int64_t u = q - (int64_t)h * s.w;
+    if (u < 0 || u >= (int64_t)ace::kMomentUMax) ++bad;
+    if (p >= exact_from && (double)q != (double)ps) ++bad;
+  }
+  return bad;
+}
+
 // Out-of-domain inputs stay in [0, n - 1] (histogram indices never leave range).
 int check_clamped(const float* table, int n) {
   const std::vector<float> tab = padded(table, n);

@@ -53,3 +53,51 @@ def onehot_np(y: torch.Tensor, channels: int, config: ACEConfig) -> np.ndarray:
         lab = y.reshape(y.shape[0], -1).numpy()
         return np.stack([(lab == c).astype(np.float64) for c in range(channels)], 1)
     return y.reshape(y.shape[0], channels, -1).double().numpy()
+
+
+def near_boundary_voxels(x: torch.Tensor, config: ACEConfig, window: float = 1e-6) -> torch.Tensor:
+    """[B, N] bool: some channel's probability lies within ``window`` of a
+    boundary where its bin assignment changes (hard: upper bin edges; soft:
+    the half boundaries, centres included, where the two bins of a voxel and
+    the sign of a weight's derivative change) -- the reference's criterion
+    (tests/test_triton.py:250-261)."""
+    from oracle import v2
+
+    p = cpu_probs(x, config).flatten(2)
+    if config.binning == "hard":
+        bounds = v2.hard_edges(config.num_bins)
+    else:
+        bounds = v2.soft_half_boundaries(config.num_bins)[1:]
+    dist = (p.unsqueeze(-1) - bounds).abs().amin(-1)
+    return (dist < window).any(1)
+
+
+def assert_grad_close(grad: torch.Tensor, grad_ref: torch.Tensor, x: torch.Tensor,
+                      config: ACEConfig, rtol: float = GRAD_RTOL, atol: float = GRAD_ATOL,
+                      truth: torch.Tensor = None) -> torch.Tensor:
+    """Gradients equal to (rtol, atol) except at voxels whose probability is
+    within 1e-6 of a bin boundary, and those rare (at most one voxel or 1e-3
+    of them): a one-ulp difference between the kernel's softmax and torch's
+    can put such a voxel on the other side (the reference's own rule,
+    tests/test_triton.py:264-296).  With ``truth`` (the float64 result), an
+    element also passes when it is at least as close to it as the float32
+    reference (to rtol, atol): elements that are small differences of large
+    terms carry the reference's own rounding.  Returns the [B, N] mask of
+    voxels that differ."""
+    g = grad.detach().cpu().float().flatten(2)
+    r = grad_ref.detach().cpu().float().flatten(2)
+    ok = torch.isclose(g, r, rtol=rtol, atol=atol)
+    if truth is not None:
+        t = truth.detach().cpu().double().flatten(2)
+        err = (g.double() - t).abs()
+        ok |= err <= (r.double() - t).abs() + rtol * t.abs() + atol
+    bad = (~ok).any(1)
+    if bad.any():
+        near = near_boundary_voxels(x, config)
+        far = bad & ~near
+        assert not far.any(), (
+            f"gradient differs away from bin boundaries at {far.nonzero()[:4].tolist()}: "
+            f"max |diff| {float((g - r).abs().max()):.3e}"
+        )
+        assert int(bad.sum()) <= max(1, int(1e-3 * bad.numel())), f"{int(bad.sum())} boundary voxels differ"
+    return bad

@@ -55,6 +55,10 @@ def harness(tmp_path_factory) -> ctypes.CDLL:
     lib.check_div.restype = ctypes.c_longlong
     lib.check_div.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                               ctypes.c_int]
+    lib.check_moment_offsets.restype = ctypes.c_longlong
+    lib.check_moment_offsets.argtypes = [fp, ctypes.c_int, ctypes.c_int]
+    lib.check_moment_all.restype = ctypes.c_longlong
+    lib.check_moment_all.argtypes = [fp, ctypes.c_int, ctypes.c_int]
     lib.check_unit_nan.restype = ctypes.c_int
     lib.check_unit_nan.argtypes = [fp, ctypes.c_int]
     return lib
@@ -165,3 +169,26 @@ def test_division_check_catches_a_missing_correction(harness) -> None:
     """Planted mistake: a * RN(1/b) without the residual correction is wrong
     for some a, and the check above reports it."""
     assert harness.check_div(_bits(1.0), _bits(1.0) + (1 << 16), 4, -30, 0, 1) > 0
+
+
+def test_soft_moment_offsets_every_bin_count(harness) -> None:
+    """The soft moments store p in half-bin h as the offset u = trunc(p 2^m)
+    - h w (``moment_scale``): u must lie in [0, 2^24) for every half-bin of
+    every bin count the moments path takes (K <= 2048), so that h w and u^2
+    are 24-bit multiplies and u^2 is exact."""
+    bad = {k: harness.check_moment_offsets(_fp(_table(k, True)), k, 0) for k in range(1, 2049)}
+    assert not any(bad.values()), {k: v for k, v in bad.items() if v}
+
+
+@pytest.mark.parametrize("planted", [1, 2])
+def test_soft_moment_offsets_check_catches_a_wrong_scale(harness, planted: int) -> None:
+    # a scale one bit too fine overflows 24 bits; a base without its margin
+    # passes the boundaries below
+    assert sum(harness.check_moment_offsets(_fp(_table(k, True)), k, planted) for k in (7, 20, 50, 333)) > 0
+
+
+@pytest.mark.parametrize("right", [False, True])
+def test_soft_moment_offsets_every_probability(harness, right: bool) -> None:
+    """Every float32 in [0, 1] at K = 20: offset in range, and base + offset
+    is exactly p 2^m for p >= 2^(23 - m)."""
+    assert harness.check_moment_all(_fp(_table(20, True)), 20, int(right)) == 0
