@@ -228,21 +228,30 @@ __device__ __forceinline__ uint32_t cvt_u32(float p30) {
 // ------------------------------------------------------------ activation
 
 // exp(x) for the softmax arguments x = logit - max <= 0: 2^(x log2 e) with
-// e = rint(x log2 e) taken out by ldexp and the reduced argument
-// a = x log2 e - e formed with one fma (exact product, one rounding: |a| <=
-// 1/2, so its rounding error is ~2^-26) plus x times the remainder of log2 e
+// e = rint(x log2 e) split off and the reduced argument a = x log2 e - e
+// formed with one fma (exact product, one rounding: |a| <= 1/2, so its
+// rounding error is ~2^-26) plus x times the remainder of log2 e
 // (log2 e = L + Llo, L its float rounding).  v_exp_f32 then sees a in
-// [-1/2, 1/2].  A clamp of x at -104, below which every result underflows,
-// keeps -inf logits finite (x <= 0 cannot overflow).  Measured on MI355X
-// against a float64 exp for every float x in [-104, 0]: max error 0.968 ulp,
-// no result off by more than 1 ulp (ROCm's expf: 0.857 / none; its range
-// reduction splits x log2 e into two terms first, two instructions more).
+// [-1/2, 1/2].  The rounding to an integer is t = fma(x, L, 1.5 2^23): t is
+// 1.5 2^23 + e exactly (|x L| < 2^22), e = t - 1.5 2^23, and since the low 9
+// bits of 1.5 2^23 are zero, (bits(t) << 23) mod 2^32 = e << 23, which one
+// integer add puts into the exponent of v_exp_f32's result (instead of
+// rint + cvt + ldexp: one instruction fewer).  That add needs a normal
+// result: x is clamped at -87 (exp(-87) = 1.6e-38, e >= -126), which also
+// keeps -inf logits finite (x <= 0 cannot overflow); below it the
+// probability is ~1e-38 either way, bin 0 and 0 in fixed point.  Measured
+// on MI355X against a float64 exp for every float x in [-87, 0]: max error
+// 0.968 ulp, no result off by more than 1 ulp (ROCm's expf: 0.857 / none;
+// its range reduction splits x log2 e into two terms first, two
+// instructions more).
 __device__ __forceinline__ float exp_neg(float x) {
-  x = fmaxf(x, -104.0f);
-  const float e = rintf(x * 0x1.715476p+0f);
+  x = fmaxf(x, -87.0f);
+  const float t = fmaf(x, 0x1.715476p+0f, 0x1.8p23f);
+  const float e = t - 0x1.8p23f;
   float a = fmaf(x, 0x1.715476p+0f, -e);
   a = fmaf(x, 0x1.4ae0bep-26f, a);
-  return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(a), (int)e);
+  const float v = __builtin_amdgcn_exp2f(a);
+  return __uint_as_float(__float_as_uint(v) + (__float_as_uint(t) << 23));
 }
 
 // In place: logits -> probabilities.  Softmax follows torch.softmax: max over
