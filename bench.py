@@ -375,7 +375,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the loss on ONE GPU; --gpus above 1 is not supported "
-              "(the path would shard voxels and all-reduce 3*B*C'*K partial sums; see DESIGN.md)",
+              "(a multi-GPU run would shard the voxels and all-reduce the 3*B*C'*K integer bin sums "
+              "before the epilogue)",
               file=sys.stderr)
         return 2
 
