@@ -109,6 +109,21 @@ int check_common(const void* x, int x_dtype, const void* target, int target_kind
 
 int to_code(hipError_t e) { return e == hipSuccess ? ACE_OK : ACE_EHIP + (int)e; }
 
+// Soft binning of softmax probabilities with label targets on a fast
+// channel count bins through half-bin moments when the bin count and the
+// moments' LDS layout (48 C'K bytes per copy, and the epilogue's terms)
+// allow it; otherwise the generic soft kernels (per-voxel weights, 24 C'K
+// bytes per copy).  Forward and backward take the same decision.
+bool use_moments(bool soft, bool labels, int act, int64_t batch, int64_t channels, int64_t voxels,
+                 int num_bins, int include_background) {
+  if (!(soft && labels && act == kActSoftmax && fast_channels(channels) &&
+        num_bins <= kMomentMaxBins))
+    return false;
+  const Geometry g = make_geometry(batch, channels, voxels, num_bins, true, include_background != 0,
+                                   true, env_steps("ACE_FWD_STEPS"), env_copies(), true);
+  return g.lds_fwd <= kMaxLds && g.lds_bwd <= kMaxLds;
+}
+
 // The activation is not an argument here: size for the larger layout (soft
 // moments when the channel count has a fast kernel and targets are labels).
 Geometry workspace_geometry(int64_t batch, int64_t channels, int64_t voxels, int num_bins,
@@ -178,9 +193,8 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   const bool soft = binning == ACE_SOFT;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
   const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
-  // soft + softmax + labels on a fast channel count: the moments kernels
-  const bool moments = soft && labels && act == kActSoftmax && fast_channels(channels) &&
-                       num_bins <= kMomentMaxBins;
+  const bool moments =
+      use_moments(soft, labels, act, batch, channels, voxels, num_bins, include_background);
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
                                    include_background != 0, labels, env_steps("ACE_FWD_STEPS"),
                                    env_copies(), moments);
@@ -253,8 +267,8 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   if (soft && !diff) return ACE_EINVAL;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
   const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
-  const bool moments = soft && labels && act == kActSoftmax && fast_channels(channels) &&
-                       num_bins <= kMomentMaxBins;
+  const bool moments =
+      use_moments(soft, labels, act, batch, channels, voxels, num_bins, include_background);
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
                                    include_background != 0, labels, env_steps("ACE_BWD_STEPS"), 0,
                                    moments);

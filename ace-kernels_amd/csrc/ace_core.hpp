@@ -1850,7 +1850,10 @@ hipError_t launch_variant_fwd(const Geometry& g, const FwdParams& prm, hipStream
 template <typename T, bool SOFT, bool RIGHT>
 hipError_t launch_variant_bwd(const Geometry& g, const BwdParams& prm, hipStream_t s);
 
-// The fast kernels serve softmax with class-index targets for C in {2, 3, 4, 16}.
+// The fast kernels serve softmax with class-index targets for C in {2, 3, 4, 16};
+// soft binning only in the moments layout (g.moments: the host declines it
+// when the bin count or its LDS size is too large, and the generic soft
+// kernels then run with their own layout).
 template <int CMAX, bool EXACT>
 constexpr bool has_fast() {
   return EXACT && (CMAX == 2 || CMAX == 3 || CMAX == 4 || CMAX == 16);
@@ -1860,7 +1863,7 @@ template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) {
   auto kern = fwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
   if constexpr (has_fast<CMAX, EXACT>()) {
-    if (prm.act == kActSoftmax && prm.tk == kTgtLabels)
+    if (prm.act == kActSoftmax && prm.tk == kTgtLabels && (!SOFT || g.moments))
       kern = prm.off ? fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true>
                      : fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false>;
   }
@@ -1879,7 +1882,7 @@ hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) 
   auto kern = bwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
   if constexpr (has_fast<CMAX, EXACT>()) {
     // the hard gradient reads no targets: any target layout takes the fast path
-    if (prm.act == kActSoftmax && (!SOFT || prm.tk == kTgtLabels))
+    if (prm.act == kActSoftmax && (!SOFT || (prm.tk == kTgtLabels && g.moments)))
       kern = prm.off ? bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true>
                      : bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false>;
   }

@@ -29,7 +29,7 @@ import pytest
 import torch
 
 from ace_kernels import ACEConfig
-from gpu_helpers import LOSS_ATOL, LOSS_RTOL, assert_grad_close, run, say
+from gpu_helpers import GRAD_ATOL, LOSS_ATOL, LOSS_RTOL, assert_grad_close, run, say
 
 pytestmark = pytest.mark.gpu
 
@@ -104,3 +104,49 @@ def test_bf16_logits(binning) -> None:
     # dx is rounded to bf16 like the input
     torch.testing.assert_close(grad.float().cpu(), grad_ref.to(torch.bfloat16).float(),
                                rtol=1e-2, atol=1e-7)
+
+
+# Many bins: soft moments while their LDS layout fits (C' K up to ~3400 at
+# 8..1 copies), the generic soft kernel beyond it (K = 1800 at C = 2, and
+# K > 2048), hard bins up to the LDS limit.  1000 voxels per batch index, so
+# most soft bins hold a voxel or two.  A soft weight moves by 2K per unit of
+# p, so one ulp of a probability moves it by ~2K * 6e-8 (2e-4 at K = 1800):
+# every voxel is sensitive, not only those near a boundary, and two float32
+# paths differ elementwise by that much.  The soft gradient is therefore held
+# to the float32 reference's own accuracy against the float64 result, in L2
+# and in the largest element (measured at K = 1800: both 6.3e-4 from float64
+# at worst, L2 1.39e-3 vs 1.40e-3).
+@pytest.mark.parametrize("binning,c,k", [
+    ("soft", 2, 300),     # moments
+    ("soft", 2, 1800),    # moments do not fit: generic soft kernel
+    ("soft", 2, 2100),    # above the moments' bin limit
+    ("hard", 4, 1000),
+    ("hard", 2, 4000),
+])
+def test_many_bins(binning, c, k) -> None:
+    cfg = ACEConfig(binning=binning, num_bins=k, to_onehot_y=True, activation="softmax")
+    x, y = _case(2, c, (25, 40), seed=k + c, onehot=True)
+    say(f"parity many bins {binning} C={c} K={k}")
+    loss, grad = run("hip_mi355x", x.cuda(), y.cuda(), cfg)
+    loss_ref, grad_ref = _oracle(x, y, cfg)
+    torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
+    if binning == "soft":
+        _, grad64 = run("reference", x.double(), y, cfg)
+        h = grad.cpu().double() - grad64
+        r = grad_ref.double() - grad64
+        assert float(h.norm()) <= 2.0 * float(r.norm()) + GRAD_ATOL * h.numel() ** 0.5, (h.norm(), r.norm())
+        assert float(h.abs().max()) <= 4.0 * float(r.abs().max()) + GRAD_ATOL, (h.abs().max(), r.abs().max())
+    else:
+        assert_grad_close(grad, grad_ref, x, cfg)
+
+
+def test_too_many_bins_raises() -> None:
+    """A layout that fits no kernel's LDS (generic soft, 24 C'K bytes per copy
+    > 160 KB) is refused on the host before any launch, with a clear error."""
+    from ace_kernels._lib import AceLibraryError
+
+    cfg = ACEConfig(binning="soft", num_bins=3000, to_onehot_y=True, activation="softmax")
+    x, y = _case(1, 4, (8, 8), seed=1, onehot=True)
+    say("unsupported: soft C=4 K=3000")
+    with pytest.raises(AceLibraryError, match="unsupported"):
+        run("hip_mi355x", x.cuda(), y.cuda(), cfg)
