@@ -1,0 +1,92 @@
+"""A seeded sweep over the option space at small sizes: every case runs the
+HIP path through the C-ABI and compares loss and gradient with the oracle's
+reference loss.  It covers channel counts 1..64 (fast and generic kernels),
+bin counts 1..64, the three activations, label and one-hot targets,
+background kept or dropped, empty classes ignored or not, the three
+reductions, right edges, and fp32 / bf16 / fp16 logits.
+
+Inputs follow the reference's domain: probabilities in [0, 1] when no
+activation applies (activation "none", or softmax over one channel), class
+indices in [0, C) or one-hot float targets.  Tolerances as the parity tests:
+loss rtol 1e-5 / atol 1e-6; gradients by the reference's rules (boundary
+voxels may differ; soft bins with fewer than 8 voxels take rtol 1e-3 or the
+float64 result); 16-bit logits are compared on the same 16-bit values, the
+gradient after rounding the oracle's to the logits' dtype.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from ace_kernels import ACEConfig
+from gpu_helpers import LOSS_ATOL, LOSS_RTOL, assert_grad_close, run, say
+
+pytestmark = pytest.mark.gpu
+
+CHANNELS = [1, 2, 3, 4, 5, 7, 8, 9, 16, 17, 33, 64]
+BINS = [1, 2, 3, 7, 20, 33, 64]
+DTYPES = [torch.float32, torch.float32, torch.float32, torch.bfloat16, torch.float16]
+
+
+def _cases(n: int = 120):
+    rng = np.random.default_rng(20261201)
+    out = []
+    for i in range(n):
+        c = int(rng.choice(CHANNELS))
+        act = str(rng.choice(["softmax", "softmax", "sigmoid", "none"]))
+        onehot = bool(rng.integers(2)) if c > 1 else False
+        kw = dict(
+            binning=str(rng.choice(["hard", "soft"])),
+            num_bins=int(rng.choice(BINS)),
+            activation=act,
+            to_onehot_y=onehot,
+            include_background=bool(rng.integers(2)),
+            ignore_empty_classes=bool(rng.integers(2)),
+            reduction=str(rng.choice(["mean", "sum", "none"])),
+            right=bool(rng.integers(2)),
+        )
+        b = int(rng.integers(1, 4))
+        spatial = tuple(int(v) for v in rng.integers(3, 17, size=int(rng.integers(1, 4))))
+        dtype = DTYPES[int(rng.integers(len(DTYPES)))]
+        out.append(pytest.param(i, b, c, spatial, dtype, kw, id=f"{i}-{kw['binning']}-C{c}-K{kw['num_bins']}-{act}"))
+    return out
+
+
+def _inputs(seed, b, c, spatial, dtype, cfg):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn((b, c, *spatial), generator=gen) * 2.0
+    if cfg.activation == "none" or (cfg.activation == "softmax" and c == 1):
+        x = torch.sigmoid(x)  # probabilities, the reference's domain without an activation
+    x = x.to(dtype)
+    labels = torch.randint(0, max(c, 2) if c == 1 else c, (b, 1, *spatial), generator=gen)
+    if cfg.to_onehot_y:
+        y = labels
+    elif c == 1:
+        y = labels.float()
+    else:
+        y = torch.zeros((b, c, *spatial)).scatter_(1, labels, 1.0)
+    return x, y
+
+
+@pytest.mark.parametrize("i,b,c,spatial,dtype,kw", _cases())
+def test_sweep(i, b, c, spatial, dtype, kw) -> None:
+    from oracle.reference import register_reference
+
+    register_reference()
+    cfg = ACEConfig(**kw)
+    x, y = _inputs(1000 + i, b, c, spatial, dtype, cfg)
+    say(f"sweep {i}: B={b} C={c} {spatial} {dtype} {kw}")
+    loss, grad = run("hip_mi355x", x.cuda(), y.cuda(), cfg)
+    loss_ref, grad_ref = run("reference", x.float(), y, cfg)
+    torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
+    if dtype != torch.float32:
+        torch.testing.assert_close(grad.float().cpu(), grad_ref.to(dtype).float(), rtol=1e-2, atol=1e-6)
+        return
+    voxels = x[0, 0].numel()
+    if cfg.binning == "soft" and voxels < 8 * cfg.num_bins:
+        _, grad64 = run("reference", x.double(), y, cfg)
+        assert_grad_close(grad, grad_ref, x, cfg, rtol=1e-3, truth=grad64)
+    else:
+        assert_grad_close(grad, grad_ref, x, cfg)
