@@ -89,7 +89,9 @@ int check_common(const void* x, int x_dtype, const void* target, int target_kind
                  int64_t batch, int64_t channels, int64_t voxels, int num_bins,
                  int binning, int activation, const float* bin_table,
                  const float* centre_table, bool need_target) {
-  if (!x || !bin_table) return ACE_EINVAL;
+  // with no voxels, input and target may be null (empty tensors): nothing
+  // reads them
+  if ((!x && voxels > 0) || !bin_table) return ACE_EINVAL;
   if (x_dtype != ACE_F32 && x_dtype != ACE_BF16 && x_dtype != ACE_F16) return ACE_EINVAL;
   if (target_kind != ACE_TARGET_LABELS_I64 && target_kind != ACE_TARGET_ONEHOT_F32)
     return ACE_EINVAL;
@@ -101,7 +103,7 @@ int check_common(const void* x, int x_dtype, const void* target, int target_kind
   if (channels > kMaxChannels) return ACE_EUNSUPPORTED;
   if (num_bins > (1 << 20)) return ACE_EUNSUPPORTED;
   if (binning == ACE_SOFT && !centre_table) return ACE_EINVAL;
-  if (need_target && !target) return ACE_EINVAL;
+  if (need_target && !target && voxels > 0) return ACE_EINVAL;
   // one channel: to_onehot_y is ignored upstream, the target is per-channel
   if (channels == 1 && target_kind == ACE_TARGET_LABELS_I64 && target) return ACE_EINVAL;
   return ACE_OK;
@@ -263,7 +265,7 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   int rc = check_common(x, x_dtype, target, target_kind, batch, channels, voxels, num_bins,
                         binning, activation, bin_table, centre_table, soft);
   if (rc) return rc;
-  if (!coef || !jac || !grad_output || !dx) return ACE_EINVAL;
+  if (!coef || !jac || !grad_output || (!dx && voxels > 0)) return ACE_EINVAL;
   if (soft && !diff) return ACE_EINVAL;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
   const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;

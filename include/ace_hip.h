@@ -17,6 +17,8 @@
  * Conventions
  *   - All pointers except `class_weight == NULL`, `stats == NULL` and the
  *     host-only arguments are device pointers on the current HIP device.
+ *     With N = 0 (no voxels) `x`, `target` and `dx` may be NULL: nothing
+ *     reads or writes them (the loss is then NaN, every bin being empty).
  *   - `stream` is a hipStream_t (0 = the null stream).  Every launch is
  *     asynchronous on it; no call synchronises, copies host<->device or
  *     allocates device memory, so both calls can be captured in a HIP graph.

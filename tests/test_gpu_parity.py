@@ -150,3 +150,20 @@ def test_too_many_bins_raises() -> None:
     say("unsupported: soft C=4 K=3000")
     with pytest.raises(AceLibraryError, match="unsupported"):
         run("hip_mi355x", x.cuda(), y.cuda(), cfg)
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+@pytest.mark.parametrize("c", [4, 5])
+def test_empty_volume(binning, c) -> None:
+    """No voxels: every bin is empty, so the class error is the mean over no
+    bins (NaN) and the loss is NaN, as in the reference; the gradient is
+    empty.  The kernels run their tiles with no voxel (first loads from a
+    dummy buffer) and must not fault."""
+    cfg = ACEConfig(binning=binning, to_onehot_y=True, activation="softmax")
+    x = torch.randn((2, c, 0, 5))
+    y = torch.zeros((2, 1, 0, 5), dtype=torch.long)
+    say(f"empty volume {binning} C={c}")
+    loss, grad = run("hip_mi355x", x.cuda(), y.cuda(), cfg)
+    loss_ref, grad_ref = _oracle(x, y, cfg)
+    torch.testing.assert_close(loss.cpu(), loss_ref, equal_nan=True)
+    assert grad.shape == grad_ref.shape == x.shape
