@@ -201,7 +201,6 @@ __device__ __forceinline__ float rcp_rn(float b) {
 }
 // div_rn(a, b, y): ace_bins.hpp (shared with the CPU test harness).
 
-// A probability already scaled by 2^30 (p in [0, 2^30] or NaN) as 30-bit
 // a * b + c with 24-bit signed a, b (v_mad_i32_i24; the compiler would
 // otherwise sign-extend a it cannot bound first).
 __device__ __forceinline__ uint32_t mad_i24(int a, int b, uint32_t c) {
@@ -217,8 +216,10 @@ __device__ __forceinline__ unsigned long long square_u24(uint32_t u) {
   return ((unsigned long long)hi << 32) | lo;
 }
 
-// fixed point, truncated: v_cvt_u32_f32 rounds toward zero and maps NaN to
-// 0.  At most 2^-30 below p.
+// A probability already scaled by 2^m (p in [0, 2^m] or NaN; m = 30 for
+// hard binning, the soft moments' scale otherwise) as m-bit fixed point,
+// truncated: v_cvt_u32_f32 rounds toward zero and maps NaN to 0.  At most
+// 2^-m below p.
 __device__ __forceinline__ uint32_t cvt_u32(float p30) {
   uint32_t q;
   asm("v_cvt_u32_f32 %0, %1" : "=v"(q) : "v"(p30));
@@ -452,13 +453,14 @@ struct Tile {
 // LDS views of one block's histogram copies.
 struct Hist {
   unsigned long long* a;  // hard: packed count | label count | sum p   [CK][R]
-                          // moments: the same per half-bin            [2CK][R]
+                          // moments: the same per half-bin, with the
+                          // offsets u of moment_scale for p           [2CK][R]
   long long* g1;          // hard + per-channel targets: sum y          [CK][R]
   long long* w;           // soft: sum of weights                       [CK][R]
   long long* p;           // soft: sum of weight * p                    [CK][R]
   long long* g;           // soft: sum of weight * y                    [CK][R]
-  unsigned long long* m2; // moments: sum p^2                           [2CK][R]
-  unsigned long long* mg; // moments: sum p over the labelled voxels    [2CK][R]
+  unsigned long long* m2; // moments: sum u^2                           [2CK][R]
+  unsigned long long* mg; // moments: sum u over the labelled voxels    [2CK][R]
 };
 
 // Adds NV voxels (logits xv, labels lab or targets yv) into the histograms.

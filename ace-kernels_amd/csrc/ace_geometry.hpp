@@ -46,15 +46,16 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 //         targets when they are per-channel values rather than labels
 //   soft: three i64 fixed-point sums W, P, G
 //   soft moments (softmax + labels): per half-bin (2K per channel) the packed
-//         word (count | label count | sum p), sum p^2 and sum p over the
-//         labelled voxels
+//         word (count | label count | sum u), sum u^2 and sum u over the
+//         labelled voxels, u the offset of the quantised p from the
+//         half-bin's base (moment_scale)
 constexpr size_t hist_bytes_per_copy(int ck, bool soft, bool labels, bool moments = false) {
   return moments ? (size_t)ck * 48 : (soft ? (size_t)ck * 24 : (size_t)ck * (labels ? 8 : 16));
 }
 
 // Final sums per batch index and replica: 3 x C'K (W, P, G per bin), or for
-// soft moments 5 x 2C'K (count, label count, sum p, sum p^2, sum p y per
-// half-bin).
+// soft moments 5 x 2C'K (count, label count, sum u, sum u^2 >> shift, sum u
+// over the labelled voxels per half-bin).
 constexpr int fin_values(int ck, bool moments) { return moments ? 10 * ck : 3 * ck; }
 
 // LDS layout of an epilogue over nb batch indices (byte offsets from the
