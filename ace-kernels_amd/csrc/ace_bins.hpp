@@ -89,13 +89,14 @@ ACE_HD int bucket_unit(float p, float nf, const float* tab) {
 // 64 bits and the sums describe the quantised values exactly (the moment
 // formulas subtract nearly equal sums, so a rounded p^2 would carry its
 // rounding, amplified by 1 / S = 2K, into P).  q is exact (p 2^m is an
-// integer) for p >= 2^(23-m): p >= 2^-5 at m = 28 (K = 16..31).  With the half boundaries e_h = h / 2K (1 + d_h), |d_h| < 8 2^-24
-// (see bucket_unit), and ws = 2^m / 2K <= 2^23:
+// integer) for p >= 2^(23-m): p >= 2^-5 at m = 28 (K = 16..31).  With the
+// half boundaries e_h = h / 2K (1 + d_h), |d_h| < 8 2^-24 (see bucket_unit),
+// and ws = 2^m / 2K <= 2^23:
 //   w <= ws (1 - 2^-14) and h w < e_h 2^m for h >= 1, so u >= 0;
 //   u <= e_{h+1} 2^m - h w < ws (1 + 2K (2^-14 + 2^-21)) + 2K
 //     < 1.26 * 2^23 + 2^12 < 2^24 = kMomentUMax for 2K <= 2^12,
 // so h w and u^2 are 24-bit multiplies (w < 2^23 fits a signed one).
-// m = 23 + floor(log2 2K) (ws > 2^22), at most 30.
+// m = 23 + floor(log2 2K), at most 30 (2^22 < ws <= 2^23 while m < 30).
 constexpr int kMomentMaxBins = 2048;
 constexpr unsigned kMomentUMax = 1u << 24;
 
