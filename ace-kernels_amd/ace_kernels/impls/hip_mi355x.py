@@ -109,19 +109,45 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False):
-    """(loss, coef, d, jac, per_class, stats-or-None) via ``ace_forward``."""
+def _stream(dev: torch.device) -> int:
+    """The current stream of ``dev`` as a raw handle (the accessor Triton
+    uses; ``torch.cuda.current_stream`` builds a Python object first)."""
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
+
+
+@lru_cache(maxsize=256)
+def _workspace_sizes(dims: Tuple[int, ...]) -> Tuple[int, int]:
+    lib = _lib.lib()
+    return lib.ace_workspace_bytes(*dims), lib.ace_workspace_reset_bytes(*dims)
+
+
+def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False, shared: bool = True):
+    """(loss, coef, d, jac, per_class, stats-or-None) via ``ace_forward``.
+    ``shared``: coef, d and jac are views of one allocation (one allocator
+    call instead of three); the custom op, whose outputs may not alias,
+    passes False."""
     lib = _lib.lib()
     dev = pl.x.device
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _stream(dev)
     binning = _lib.SOFT if pl.soft else _lib.HARD
     dims = (pl.B, pl.C, pl.N, pl.K, binning, pl.dtype_code, int(pl.include_bg), pl.target_kind)
-    ws = workspace(dev, stream, lib.ace_workspace_bytes(*dims), lib.ace_workspace_reset_bytes(*dims))
+    ws = workspace(dev, stream, *_workspace_sizes(dims))
     f32 = torch.float32
-    coef = torch.empty((pl.B, pl.CL, pl.K), dtype=f32, device=dev)
-    d = torch.empty_like(coef)
-    jac = torch.empty((pl.B, pl.CL), dtype=f32, device=dev)
-    per_class = torch.empty_like(jac)
+    # coef, d and jac (all saved for backward) share one allocation; the
+    # per-class errors and the loss, which the caller may receive and modify
+    # in place, have their own
+    bck, bc = pl.B * pl.CL * pl.K, pl.B * pl.CL
+    if shared:
+        saved = torch.empty(2 * bck + bc, dtype=f32, device=dev)
+        coef = saved[:bck].view(pl.B, pl.CL, pl.K)
+        d = saved[bck:2 * bck].view(pl.B, pl.CL, pl.K)
+        jac = saved[2 * bck:].view(pl.B, pl.CL)
+    else:
+        coef = torch.empty((pl.B, pl.CL, pl.K), dtype=f32, device=dev)
+        d = torch.empty_like(coef)
+        jac = torch.empty((pl.B, pl.CL), dtype=f32, device=dev)
+    per_class = torch.empty((pl.B, pl.CL), dtype=f32, device=dev)
     reduction = _REDUCTIONS[config.reduction]
     loss = torch.empty((), dtype=f32, device=dev) if reduction != _lib.RED_NONE else None
     st = torch.empty((3, pl.B, pl.CL, pl.K), dtype=torch.float64, device=dev) if stats else None
@@ -147,7 +173,7 @@ def hip_backward(pl: Plan, coef: torch.Tensor, d: torch.Tensor, jac: torch.Tenso
     """d loss / d input (input's shape and dtype) via ``ace_backward``."""
     lib = _lib.lib()
     dev = pl.x.device
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _stream(dev)
     per_class = grad_output.dim() > 0
     go = grad_output
     if go.dtype != torch.float32:
@@ -236,7 +262,7 @@ config_arg = torch.compiler.assume_constant_result(_dump)
 def hip_forward_op(input: torch.Tensor, target: torch.Tensor, config_json: str) -> Outputs:
     """mL1-ACE forward: (loss, coef, d, jac) from one ``ace_forward`` launch."""
     config = _config(config_json)
-    loss, coef, d, jac, _, _ = hip_forward(make_plan(input, target, config), config)
+    loss, coef, d, jac, _, _ = hip_forward(make_plan(input, target, config), config, shared=False)
     # a custom op may not return a view of an internal buffer: copy the "none" view
     return (loss.clone() if loss.dim() else loss), coef, d, jac
 
