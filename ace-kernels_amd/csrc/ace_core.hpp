@@ -673,15 +673,8 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
       const int bb = nb == 1 ? 0 : t / H2;
       const int th = t - bb * H2;
       unsigned long long* fb = P.fin + (int64_t)(b0 + bb) * reps * NV;
-      long long m[5] = {0, 0, 0, 0, 0};
-#pragma unroll
-      for (int r = 0; r < kMaxReps; ++r) {
-        if (r < reps) {
-          unsigned long long* f = fb + (int64_t)r * NV;
-#pragma unroll
-          for (int v = 0; v < 5; ++v) m[v] += (long long)load_dev(&f[v * H2 + th]);
-        }
-      }
+      long long m[5];
+      load_sums<5>(fb, NV, reps, H2, th, m);  // every replica's loads in flight at once
       zero_sums<5>(fb, NV, reps, H2, th);
       const int hh = th % (2 * K);
       const double L = (double)((long long)hh * P.mw) * mscale;
