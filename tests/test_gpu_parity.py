@@ -167,3 +167,38 @@ def test_empty_volume(binning, c) -> None:
     loss_ref, grad_ref = _oracle(x, y, cfg)
     torch.testing.assert_close(loss.cpu(), loss_ref, equal_nan=True)
     assert grad.shape == grad_ref.shape == x.shape
+
+
+# Input layouts and target dtypes the callers hand over: a strided slice and a
+# channels-last tensor (copied to the kernels' [B, C, N] layout), int32 and
+# float class labels (read as int64, as the reference's `.long()`,
+# impls/v5_triton.py:25-32), float64 one-hot targets (read as float32).  The
+# gradient has the caller's shape.
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+@pytest.mark.parametrize("variant", ["slice", "channels_last", "int32_labels", "float_labels",
+                                     "f64_onehot"])
+def test_input_layouts_and_target_dtypes(binning, variant) -> None:
+    onehot = variant != "f64_onehot"
+    cfg = ACEConfig(binning=binning, to_onehot_y=onehot, activation="softmax")
+    x, y = _case(2, 4, (10, 9, 8), seed=17, onehot=onehot)
+    xg, yg = x.cuda(), y.cuda()
+    if variant == "slice":
+        big = torch.randn((2, 4, 20, 9, 8)).cuda()
+        big[:, :, ::2] = xg
+        xg = big[:, :, ::2]
+        assert not xg.is_contiguous()
+    elif variant == "channels_last":
+        xg = xg.contiguous(memory_format=torch.channels_last_3d)
+        assert not xg.is_contiguous()
+    elif variant == "int32_labels":
+        yg = yg.int()
+    elif variant == "float_labels":
+        yg = yg.float()
+    else:
+        yg = yg.double()
+    say(f"layout {binning} {variant}")
+    loss, grad = run("hip_mi355x", xg, yg, cfg)
+    loss_ref, grad_ref = _oracle(x, y, cfg)
+    torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
+    assert grad.shape == x.shape
+    assert_grad_close(grad, grad_ref, x, cfg)
