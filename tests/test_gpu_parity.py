@@ -202,3 +202,20 @@ def test_input_layouts_and_target_dtypes(binning, variant) -> None:
     torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
     assert grad.shape == x.shape
     assert_grad_close(grad, grad_ref, x, cfg)
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+@pytest.mark.parametrize("c", [4, 5])
+def test_per_class_upstream_gradient(binning, c) -> None:
+    """Reduction "none" with a different upstream gradient per class row, the
+    reference's `linspace(0.5, 2.0)` (tests/test_triton.py:283-285): the
+    backward scales each row's coefficients by its own upstream value."""
+    cfg = ACEConfig(binning=binning, to_onehot_y=True, activation="softmax", reduction="none",
+                    include_background=False)
+    x, y = _case(3, c, (9, 8, 7), seed=23, onehot=True)
+    say(f"per-class upstream {binning} C={c}")
+    up = torch.linspace(0.5, 2.0, 3 * (c - 1))
+    loss, grad = run("hip_mi355x", x.cuda(), y.cuda(), cfg, upstream=up)
+    loss_ref, grad_ref = run("reference", x, y, cfg, upstream=up)
+    torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
+    assert_grad_close(grad, grad_ref, x, cfg)
