@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # enums of include/ace_hip.h
 F32, BF16, F16 = 0, 1, 2
@@ -31,6 +31,7 @@ EXPORTS = (
     "ace_workspace_reset_bytes",
     "ace_forward",
     "ace_backward",
+    "ace_set_launch_events",
 )
 
 _p = ctypes.c_void_p
@@ -84,6 +85,8 @@ def lib() -> ctypes.CDLL:
         _p, _i,                    # grad_output, per_class
         _p, _p,                    # dx, stream
     ]
+    handle.ace_set_launch_events.restype = _i
+    handle.ace_set_launch_events.argtypes = [_p, _p]
     version = handle.ace_abi_version()
     if version != ABI_VERSION:
         raise AceLibraryError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}: rebuild it")

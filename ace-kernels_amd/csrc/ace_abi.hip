@@ -144,7 +144,7 @@ using namespace ace;
 
 extern "C" {
 
-int ace_abi_version(void) { return 2; }
+int ace_abi_version(void) { return 3; }
 
 const char* ace_error_string(int code) {
   switch (code) {
@@ -307,6 +307,11 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   p.go = grad_output;
 
   return to_code(dispatch_bwd(x_dtype, soft, right != 0, g, p, static_cast<hipStream_t>(stream)));
+}
+
+int ace_set_launch_events(void* start, void* stop) {
+  launch_events() = LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
+  return ACE_OK;
 }
 
 }  // extern "C"

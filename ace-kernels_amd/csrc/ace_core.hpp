@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 #include "ace_bins.hpp"
@@ -1854,6 +1855,30 @@ constexpr bool has_fast() {
   return EXACT && (CMAX == 2 || CMAX == 3 || CMAX == 4 || CMAX == 16);
 }
 
+// Events stamped by the kernels launched from the calling thread
+// (ace_set_launch_events): start as the dispatch begins, stop as it ends.
+struct LaunchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+inline LaunchEvents& launch_events() {
+  static thread_local LaunchEvents ev;
+  return ev;
+}
+
+// One launch of `kern` (one by-value parameter block) on kThreads-thread blocks.
+template <typename Kern, typename Params>
+hipError_t launch(Kern kern, long long nblk, size_t lds, hipStream_t s, const Params& prm) {
+  const LaunchEvents& ev = launch_events();
+  if (ev.start || ev.stop) {
+    void* args[] = {const_cast<Params*>(&prm)};
+    return hipExtLaunchKernel(reinterpret_cast<const void*>(kern), dim3((unsigned)nblk),
+                              dim3(kThreads), args, lds, s, ev.start, ev.stop, 0);
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(kThreads), lds, s, prm);
+  return hipGetLastError();
+}
+
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) {
   auto kern = fwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
@@ -1868,8 +1893,7 @@ hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) 
                                        (int)g.lds_fwd);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)g.nblk), dim3(kThreads), g.lds_fwd, s, prm);
-  return hipGetLastError();
+  return launch(kern, g.nblk, g.lds_fwd, s, prm);
 }
 
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
@@ -1887,8 +1911,7 @@ hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) 
                                        (int)g.lds_bwd);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)g.nblk), dim3(kThreads), g.lds_bwd, s, prm);
-  return hipGetLastError();
+  return launch(kern, g.nblk, g.lds_bwd, s, prm);
 }
 
 // Instantiates the per-variant switch for one (element type, binning, right).

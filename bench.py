@@ -16,8 +16,11 @@ method, ``src/ace_bench/timing.py:48-77``); a HIP-graph replay of the same step
 is reported beside it, and forward and backward kernels are also timed alone.
 
 ``roofline`` is for the dominant kernel: achieved = its algorithmic bytes per
-launch / its mean duration over the timed launches (events around each
-launch, cold cache).  ``traffic`` is read from the committed rocprofv3
+launch / its mean duration over the timed launches (cold cache; HIP events
+that the kernel's dispatch stamps as it starts and ends, through
+``ace_set_launch_events``, so they agree with rocprofv3's kernel durations;
+events recorded on the stream around the same launches, which add the
+dispatch gap after the flush, are reported beside them).  ``traffic`` is read from the committed rocprofv3
 FETCH_SIZE / WRITE_SIZE summary when there is one.  ``cpu_baseline`` times the
 reference algorithm (restated in ``oracle/``) fwd+bwd on configuration 2 on
 the host CPU.
@@ -95,6 +98,37 @@ def time_steps(fn, steps: int, warmup: int, flush):
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
+def time_kernel_steps(fn, steps: int, warmup: int, flush):
+    """Per-call duration (ms) of the one kernel ``fn`` launches through the
+    C-ABI, cold (flush before each call): the kernel stamps the two events
+    itself (``ace_set_launch_events``), so the time excludes the dispatch
+    gap after the flush that events recorded on the stream include."""
+    import torch
+
+    from ace_kernels import _lib
+
+    for _ in range(warmup):
+        flush()
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for s, e in zip(starts, ends):
+        s.record()  # creates the events; the launch re-stamps them
+        e.record()
+    torch.cuda.synchronize()
+    try:
+        for s, e in zip(starts, ends):
+            flush()
+            _lib.check(_lib.lib().ace_set_launch_events(s.cuda_event, e.cuda_event),
+                       "ace_set_launch_events")
+            fn()
+    finally:
+        _lib.lib().ace_set_launch_events(None, None)
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
 def time_back_to_back(fn, launches: int, warmup: int):
     """Mean ms per call of ``fn`` issued back to back (events around the loop)."""
     import torch
@@ -154,8 +188,11 @@ def bench_workload(wl, steps: int, warmup: int, flush):
     flush()
     loss, coef, d, jac, _, _ = hip.hip_forward(pl, cfg)
     go = torch.ones((), device="cuda")
-    fwd_cold = time_steps(lambda: hip.hip_forward(pl, cfg), steps, warmup, flush)
-    bwd_cold = time_steps(lambda: hip.hip_backward(pl, coef, d, jac, go), steps, warmup, flush)
+    fwd_cold = time_kernel_steps(lambda: hip.hip_forward(pl, cfg), steps, warmup, flush)
+    bwd_cold = time_kernel_steps(lambda: hip.hip_backward(pl, coef, d, jac, go), steps, warmup,
+                                 flush)
+    # the same launches timed by events recorded on the stream around them
+    fwd_stream = time_steps(lambda: hip.hip_forward(pl, cfg), steps, warmup, flush)
     fwd_ms = statistics.fmean(fwd_cold)
     bwd_ms = statistics.fmean(bwd_cold)
 
@@ -175,6 +212,7 @@ def bench_workload(wl, steps: int, warmup: int, flush):
         "eager_ms": _quantiles(eager),
         "fwd_ms": _quantiles(fwd_cold),
         "bwd_ms": _quantiles(bwd_cold),
+        "fwd_ms_stream_events": _quantiles(fwd_stream),
         "fwd_GBps": wl.ideal_bytes("fwd") / (statistics.median(fwd_cold) * 1e-3) / 1e9,
         "graph_replay_matches_eager": graph_ok,
         "loss": float(loss.item()),

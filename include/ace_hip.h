@@ -126,6 +126,19 @@ int ace_backward(const void* x, int x_dtype, const void* target,
                  const float* grad_output, int grad_output_per_class,
                  void* dx, void* stream);
 
+/*
+ * Kernel timing.  This has no counterpart in the reference, whose benchmark
+ * brackets each call with events recorded on the stream
+ * (src/ace_bench/timing.py:48-77); on HIP such events also time the dispatch
+ * of the kernel after the work before it.  While set, every kernel that
+ * ace_forward / ace_backward launch from the calling thread stamps `start`
+ * (a hipEvent_t, or NULL) as it begins and `stop` as it ends
+ * (hipExtLaunchKernel), so the events' elapsed time is the kernel's own
+ * duration; a call that launches several kernels leaves the last one's.
+ * ace_set_launch_events(NULL, NULL) turns it off.  Returns ACE_OK.
+ */
+int ace_set_launch_events(void* start, void* stop);
+
 #ifdef __cplusplus
 }
 #endif
