@@ -136,3 +136,46 @@ def test_no_host_synchronisation(binning) -> None:
     finally:
         torch.cuda.set_sync_debug_mode("default")
     assert torch.isfinite(g).all()
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_kernel_stamped_timing_events(binning) -> None:
+    """ace_set_launch_events: the forward and backward kernels stamp two
+    events (their elapsed time is positive and at most that of events
+    recorded on the stream around the same call), the results do not change,
+    and clearing the events restores the plain launch."""
+    from ace_kernels import _lib
+
+    x, y = _inputs(7, shape=(2, 4, 32, 32, 32))
+    cfg = ACEConfig(binning=binning, to_onehot_y=True)
+    leaf = x.detach().clone().requires_grad_(True)
+
+    def step():
+        loss = ace_loss(leaf, y, cfg, impl="hip_mi355x")
+        (g,) = torch.autograd.grad(loss.sum(), leaf)
+        return loss.detach(), g
+
+    want_loss, want_grad = step()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in ev:
+        e.record()
+    torch.cuda.synchronize()
+    say(f"stamped events {binning}")
+    ev[0].record()
+    try:
+        _lib.check(_lib.lib().ace_set_launch_events(ev[1].cuda_event, ev[2].cuda_event),
+                   "ace_set_launch_events")
+        loss = ace_loss(leaf, y, cfg, impl="hip_mi355x")
+    finally:
+        _lib.lib().ace_set_launch_events(None, None)
+    ev[3].record()
+    (g,) = torch.autograd.grad(loss.sum(), leaf)
+    torch.cuda.synchronize()
+    kernel_ms = ev[1].elapsed_time(ev[2])
+    around_ms = ev[0].elapsed_time(ev[3])
+    say(f"forward kernel {kernel_ms * 1e3:.1f} us, stream events {around_ms * 1e3:.1f} us")
+    assert 0.0 < kernel_ms <= around_ms
+    assert torch.equal(loss.detach(), want_loss)
+    assert torch.equal(g, want_grad)
+    again_loss, again_grad = step()
+    assert torch.equal(again_loss, want_loss) and torch.equal(again_grad, want_grad)
