@@ -219,3 +219,31 @@ def test_per_class_upstream_gradient(binning, c) -> None:
     loss_ref, grad_ref = run("reference", x, y, cfg, upstream=up)
     torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
     assert_grad_close(grad, grad_ref, x, cfg)
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+@pytest.mark.parametrize("c", [4, 5])
+def test_labels_naming_no_channel(binning, c) -> None:
+    """Class labels outside [0, C) (-1, C, 2^32 + 1) name no channel: the
+    voxel's one-hot target row is all zero, as in the reference's v6 kernels
+    (`label == c` per channel, kernels/hard_hist.py:88,108).  Checked against
+    the oracle given that all-zero one-hot target (to_onehot_y=False) and
+    against the HIP path given the same one-hot target."""
+    x, y = _case(2, c, (9, 8, 7), seed=29, onehot=True)
+    gen = torch.Generator().manual_seed(30)
+    odd = torch.rand(y.shape, generator=gen) < 0.2
+    bad = torch.tensor([-1, c, (1 << 32) + 1])[torch.randint(0, 3, y.shape, generator=gen)]
+    y = torch.where(odd, bad, y)
+    onehot = torch.zeros((2, c, 9, 8, 7))
+    ok = (y >= 0) & (y < c)
+    onehot.scatter_(1, torch.where(ok, y, 0), ok.float())
+    cfg_lab = ACEConfig(binning=binning, to_onehot_y=True, activation="softmax")
+    cfg_hot = ACEConfig(binning=binning, to_onehot_y=False, activation="softmax")
+    say(f"labels naming no channel {binning} C={c}: {int(odd.sum())} voxels")
+    loss, grad = run("hip_mi355x", x.cuda(), y.cuda(), cfg_lab)
+    loss_hot, grad_hot = run("hip_mi355x", x.cuda(), onehot.cuda(), cfg_hot)
+    loss_ref, grad_ref = _oracle(x, onehot, cfg_hot)
+    torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
+    assert_grad_close(grad, grad_ref, x, cfg_lab)
+    torch.testing.assert_close(loss, loss_hot, rtol=LOSS_RTOL, atol=LOSS_ATOL)
+    assert_grad_close(grad, grad_hot.cpu(), x, cfg_lab)
