@@ -135,7 +135,8 @@ int ace_backward(const void* x, int x_dtype, const void* target,
  * (a hipEvent_t, or NULL) as it begins and `stop` as it ends
  * (hipExtLaunchKernel), so the events' elapsed time is the kernel's own
  * duration; a call that launches several kernels leaves the last one's.
- * ace_set_launch_events(NULL, NULL) turns it off.  Returns ACE_OK.
+ * ace_set_launch_events(NULL, NULL) turns it off.  Meant for timing eager
+ * calls: turn it off before capturing calls into a HIP graph.  Returns ACE_OK.
  */
 int ace_set_launch_events(void* start, void* stop);
 
