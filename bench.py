@@ -491,7 +491,7 @@ def main() -> int:
         "hard_bin_parity": parity,
     }
     if not args.no_cpu:
-        log("cpu baseline (oracle reference, cfg1)")
+        log("cpu baseline (oracle reference, cfg 2)")
         line["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(line), flush=True)
     return 0
