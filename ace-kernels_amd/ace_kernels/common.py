@@ -79,11 +79,11 @@ def workspace(device: torch.device, stream: int, nbytes: int, reset_bytes: int) 
 
     One buffer per (device, stream): forwards on one stream are ordered, so
     they share it; forwards on different streams get different buffers.  Every
-    forward leaves its own reset region (ticket counters and final sums) zero
-    and writes its per-block partials right after it, so the leading
-    ``clean`` bytes of the buffer are known to be zero, where ``clean`` is the
-    reset size of the last forward; a forward that needs more is preceded by
-    one fill of its reset region (only when the problem's layout grows).
+    forward leaves its reset region (ticket counters, loss partial words and
+    final sums) zero, so the leading ``clean`` bytes of the buffer are known
+    to be zero, where ``clean`` is the reset size of the last forward; a
+    forward that needs more is preceded by one fill of its reset region (only
+    when the problem's layout grows).
     """
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     with _WS_LOCK:

@@ -1,0 +1,54 @@
+"""Many forwards in a row on one workspace: every launch's cross-block
+protocol (final-sum atomics, ticket counters reset by the block that draws
+the last ticket, loss partial words published and polled) must leave the
+workspace zero for the next launch, so repeated launches give bit-identical
+results and the workspace is all zero afterwards.  Covers the benchmark shape
+(one epilogue per batch index, loss polled from B = 2 partial words), a
+single batch index (one epilogue for everything) and B = 65 (partial words
+polled in two chunks), hard and soft."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from ace_kernels import ACEConfig
+from ace_kernels import common
+from ace_kernels.impls import hip_mi355x as hip
+from gpu_helpers import say
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    # (batch, channels, spatial, launches)
+    (2, 4, (128, 128, 128), 1000),
+    (1, 4, (64, 64, 64), 2000),
+    (65, 2, (16, 16, 8), 2000),
+]
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+@pytest.mark.parametrize("b,c,spatial,launches", SHAPES)
+def test_repeated_forwards_are_identical_and_leave_the_workspace_zero(binning, b, c, spatial,
+                                                                      launches) -> None:
+    gen = torch.Generator().manual_seed(41)
+    x = (torch.randn((b, c, *spatial), generator=gen) * 2.0).cuda()
+    y = torch.randint(0, c, (b, 1, *spatial), generator=gen).cuda()
+    cfg = ACEConfig(binning=binning, to_onehot_y=True, activation="softmax")
+    pl = hip.make_plan(x, y, cfg)
+    say(f"repeat {binning} B={b} C={c} {spatial}: {launches} forwards")
+    first = hip.hip_forward(pl, cfg)
+    want_loss, want_coef, want_d = first[0].clone(), first[1].clone(), first[2].clone()
+    losses = torch.empty(launches, dtype=torch.float32, device="cuda")
+    bad_coef = torch.zeros((), dtype=torch.int64, device="cuda")
+    for i in range(launches):
+        loss, coef, d, _, _, _ = hip.hip_forward(pl, cfg)
+        losses[i] = loss
+        bad_coef += (coef != want_coef).sum() + (d != want_d).sum()
+    torch.cuda.synchronize()
+    say(f"repeat {binning} B={b}: done")
+    assert torch.equal(losses, want_loss.expand(launches)), losses[losses != want_loss][:8]
+    assert int(bad_coef) == 0
+    stream = torch.cuda.current_stream().cuda_stream
+    ws = common._WORKSPACES[(torch.cuda.current_device(), stream)][0]
+    assert int(torch.count_nonzero(ws)) == 0
