@@ -10,9 +10,9 @@
   later calls are.
 - Class weights are validated on the Python config values exactly as
   ``common.class_weights`` (``common.py:162-181``) and cached on the device.
-- The forward's workspace (per-block partial sums + ticket counters) is cached
-  per (device, stream) and grown on demand; its counters are zero when
-  created and every forward leaves them zero.
+- The forward's workspace (ticket counters, loss partial words, final sums)
+  is cached per (device, stream) and grown on demand; it is zero when created
+  and every forward leaves it zero.
 """
 
 from __future__ import annotations
