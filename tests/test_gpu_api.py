@@ -179,3 +179,35 @@ def test_kernel_stamped_timing_events(binning) -> None:
     assert torch.equal(g, want_grad)
     again_loss, again_grad = step()
     assert torch.equal(again_loss, want_loss) and torch.equal(again_grad, want_grad)
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_concurrent_streams(binning) -> None:
+    """Forwards and backwards issued on two streams at once use one workspace
+    per stream and share no device state: every result equals the one
+    computed alone on the default stream."""
+    cfg = ACEConfig(binning=binning, to_onehot_y=True)
+    inputs = [_inputs(10 + i, shape=(2, 4, 32, 32, 32)) for i in range(2)]
+    leaves = [x.detach().clone().requires_grad_(True) for x, _ in inputs]
+
+    def step(i):
+        loss = ace_loss(leaves[i], inputs[i][1], cfg, impl="hip_mi355x")
+        (g,) = torch.autograd.grad(loss.sum(), leaves[i])
+        return loss.detach(), g
+
+    want = [step(i) for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    say(f"concurrent streams {binning}")
+    got = [[], []]
+    for _ in range(20):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                got[i].append(step(i))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for loss, g in got[i]:
+            assert torch.equal(loss, want[i][0])
+            assert torch.equal(g, want[i][1])
