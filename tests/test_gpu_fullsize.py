@@ -1,13 +1,20 @@
-"""Loss and gradient at the benchmark sizes (configurations 2 and 3: B=2, C=4,
-128^3 fp32, K=20, hard and soft), against the CPU restatement of the reference
-and against a float64 truth, as the reference's harness reports them
-(``src/ace_bench/measure.py:142-212``; its own float32 error grows with N,
-``docs/report.md:629-633``).
+"""Loss and gradient at the benchmark sizes (configurations 1 to 5: up to 8.4 M
+voxels, C up to 16, K 20 and 50, fp32 and bf16 logits, hard and soft),
+against the CPU restatement of the reference and against a float64 truth, as
+the reference's harness reports them (``src/ace_bench/measure.py:142-212``;
+its own float32 error grows with N, ``docs/report.md:629-633``).
 
 Bars: against the float32 reference, the north-star tolerances (loss rtol
 1e-5, gradient relative L2 1e-4); against the float64 truth, the kernels'
 error must not exceed twice the float32 reference's own (or 1e-6 relative,
-whichever is larger)."""
+whichever is larger).  With bf16 logits the reference and the truth compute
+on the same bf16 values, and since dx is bf16 like the input, their
+gradients are rounded to bf16 before they are compared.  There an element
+whose float32 value lies near a bf16 rounding boundary can round one bf16 ulp
+(2^-8 relative) either way, so the gradient bar against the reference is the
+larger of 1e-4 and the reference's own distance from the truth (measured at
+cfg 5: kernels 1.7e-4 from the reference, 3.0e-4 from the truth; the
+reference 3.4e-4 from the truth)."""
 
 from __future__ import annotations
 
@@ -22,7 +29,7 @@ from gpu_helpers import run, say
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("index", [2, 3])
+@pytest.mark.parametrize("index", [1, 2, 3, 4, 5])
 def test_benchmark_size_against_reference_and_truth(index) -> None:
     from oracle.reference import register_reference
     from oracle.v2 import register_v2
@@ -36,12 +43,14 @@ def test_benchmark_size_against_reference_and_truth(index) -> None:
     loss, grad = run("hip_mi355x", x.cuda(), y.cuda(), cfg)
     loss, grad = loss.cpu(), grad.cpu()
     say(f"full size {wl.name}: CPU reference (float32)")
-    loss_ref, grad_ref = run("reference", x, y, cfg)
+    loss_ref, grad_ref = run("reference", x.float(), y, cfg)
     say(f"full size {wl.name}: float64 truth")
     leaf = x.double().requires_grad_(True)
     loss64 = ace_loss(leaf, y, cfg, impl="v2_recompute")
     (grad64,) = torch.autograd.grad(loss64.sum(), leaf)
     loss64, grad64 = loss64.detach(), grad64.detach()
+    if x.dtype != torch.float32:  # dx has the input's type
+        grad_ref, grad64 = grad_ref.to(x.dtype), grad64.to(x.dtype)
 
     err = {
         "loss_vs_ref": rel_err(loss, loss_ref),
@@ -54,6 +63,7 @@ def test_benchmark_size_against_reference_and_truth(index) -> None:
     say(f"full size {wl.name}: loss {float(loss):.9g} (truth {float(loss64):.9g}) "
         + " ".join(f"{k} {v:.2e}" for k, v in err.items()))
     assert err["loss_vs_ref"] < 1e-5
-    assert err["grad_l2_vs_ref"] < 1e-4
+    grad_bar = 1e-4 if x.dtype == torch.float32 else max(1e-4, err["ref_grad_l2_vs_truth"])
+    assert err["grad_l2_vs_ref"] < grad_bar
     assert err["loss_vs_truth"] <= max(2 * err["ref_loss_vs_truth"], 1e-6)
     assert err["grad_l2_vs_truth"] <= max(2 * err["ref_grad_l2_vs_truth"], 1e-6)
