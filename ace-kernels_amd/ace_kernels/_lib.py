@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # enums of include/ace_hip.h
 F32, BF16, F16 = 0, 1, 2
@@ -32,6 +32,9 @@ EXPORTS = (
     "ace_forward",
     "ace_backward",
     "ace_set_launch_events",
+    "ace_workspace_bytes_levels",
+    "ace_forward_levels",
+    "ace_backward_levels",
 )
 
 _p = ctypes.c_void_p
@@ -39,6 +42,20 @@ _i = ctypes.c_int
 _i64 = ctypes.c_int64
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
+
+
+class AceFwdLevel(ctypes.Structure):
+    """struct AceFwdLevel of include/ace_hip.h."""
+
+    _fields_ = [("x", _p), ("target", _p), ("voxels", _i64), ("coef", _p), ("diff", _p),
+                ("jac", _p), ("per_class", _p), ("loss", _p)]
+
+
+class AceBwdLevel(ctypes.Structure):
+    """struct AceBwdLevel of include/ace_hip.h."""
+
+    _fields_ = [("x", _p), ("target", _p), ("voxels", _i64), ("coef", _p), ("diff", _p),
+                ("jac", _p), ("grad_output", _p), ("dx", _p)]
 
 
 class AceLibraryError(RuntimeError):
@@ -84,6 +101,22 @@ def lib() -> ctypes.CDLL:
         _p, _p, _p,                # coef, diff, jac
         _p, _i,                    # grad_output, per_class
         _p, _p,                    # dx, stream
+    ]
+    handle.ace_workspace_bytes_levels.restype = _sz
+    handle.ace_workspace_bytes_levels.argtypes = [_i, ctypes.POINTER(_i64), _i64, _i64, _i, _i, _i, _i]
+    handle.ace_forward_levels.restype = _i
+    handle.ace_forward_levels.argtypes = [
+        _i, ctypes.POINTER(AceFwdLevel), _i,   # levels, per-level pointers, dtype
+        _i64, _i64, _i, _i, _i,                # B, C, K, binning, include_bg
+        _i, _i, _i, _f,                        # ignore_empty, reduction, right, empty_weight
+        _p, _p, _p,                            # class_weight, bin_table, centre_table
+        _p, _sz, _p,                           # workspace, bytes, stream
+    ]
+    handle.ace_backward_levels.restype = _i
+    handle.ace_backward_levels.argtypes = [
+        _i, ctypes.POINTER(AceBwdLevel), _i,
+        _i64, _i64, _i, _i, _i, _i, _i,        # B, C, K, binning, include_bg, right, per_class
+        _p, _p, _p,                            # bin_table, centre_table, stream
     ]
     handle.ace_set_launch_events.restype = _i
     handle.ace_set_launch_events.argtypes = [_p, _p]

@@ -18,7 +18,11 @@ namespace ace {
   template <> hipError_t launch_variant_fwd<T, SOFT, RIGHT>(const Geometry&, const FwdParams&, \
                                                             hipStream_t);                    \
   template <> hipError_t launch_variant_bwd<T, SOFT, RIGHT>(const Geometry&, const BwdParams&, \
-                                                            hipStream_t);
+                                                            hipStream_t);                    \
+  template <> hipError_t launch_levels_fwd<T, SOFT, RIGHT>(int, long long, size_t,             \
+                                                           const FwdLevels&, hipStream_t);   \
+  template <> hipError_t launch_levels_bwd<T, SOFT, RIGHT>(int, long long, size_t,             \
+                                                           const BwdLevels&, hipStream_t);
 #define ACE_DECLARE_BOTH(T, SOFT) ACE_DECLARE_LAUNCHERS(T, SOFT, false) ACE_DECLARE_LAUNCHERS(T, SOFT, true)
 ACE_DECLARE_BOTH(float, false)
 ACE_DECLARE_BOTH(float, true)
@@ -137,6 +141,131 @@ Geometry workspace_geometry(int64_t batch, int64_t channels, int64_t voxels, int
                        soft && labels && fast_channels(channels));
 }
 
+// Kernel parameters of one forward problem (geometry g, workspace at ws).
+FwdParams fwd_params(const void* x, int x_dtype, const void* target, bool labels, int64_t voxels,
+                     int64_t batch, int64_t channels, int num_bins, int act,
+                     int ignore_empty_classes, int reduction, float empty_weight, bool moments,
+                     const float* class_weight, const float* bin_table, const float* centre_table,
+                     void* workspace, const Geometry& g, float* coef, float* diff, float* jac,
+                     float* per_class, float* loss, double* stats) {
+  const int vec = g.var.vec;
+  const size_t es = elem_size(x_dtype);
+  const bool vec_ok = (voxels % vec) == 0 && aligned_to(x, es * vec) &&
+                      (labels ? aligned_to(target, 16) : aligned_to(target, 4 * vec));
+
+  FwdParams p{};
+  p.x = x;
+  p.tgt = target;
+  p.N = voxels;
+  p.tile_vox = g.tile_vox;
+  p.tiles = g.tiles;
+  p.gs = g.gs;
+  p.gpb = g.gpb;
+  p.B = (int)batch;
+  p.C = (int)channels;
+  p.off = g.off;
+  p.K = num_bins;
+  p.act = act;
+  p.tk = labels ? kTgtLabels : kTgtOnehot;
+  p.copies = g.copies;
+  p.vec_ok = vec_ok ? 1 : 0;
+  p.ignore_empty = ignore_empty_classes != 0;
+  p.red = reduction;
+  p.empty_w = empty_weight;
+  if (moments) {
+    const MomentScale ms = moment_scale(num_bins);
+    p.msc = ldexpf(1.0f, ms.m);
+    p.misc = ldexpf(1.0f, -ms.m);
+    p.mw = ms.w;
+    p.mshift = moment_shift(voxels);
+  }
+  p.btab = bin_table;
+  p.rtab = centre_table;
+  p.clsw = class_weight;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  p.ctr = reinterpret_cast<int*>(ws);
+  p.part = reinterpret_cast<unsigned long long*>(ws + g.off_part);
+  p.fin = reinterpret_cast<unsigned long long*>(ws + g.off_fin);
+  p.reps = g.reps;
+  p.lchunk = g.lchunk;
+  p.epi_all = g.epi_all ? 1 : 0;
+  p.coef = coef;
+  p.d = diff;
+  p.jac = jac;
+  p.f = per_class;
+  p.loss = loss;
+  p.stats = stats;
+
+  return p;
+}
+
+// Kernel parameters of one backward problem (geometry g).
+BwdParams bwd_params(const void* x, int x_dtype, const void* target, bool labels, bool soft,
+                     int64_t voxels, int64_t batch, int64_t channels, int num_bins, int act,
+                     const float* bin_table, const float* centre_table, const float* coef,
+                     const float* diff, const float* jac, const float* grad_output,
+                     int grad_output_per_class, void* dx, const Geometry& g) {
+  const int vec = g.var.vec;
+  const size_t es = elem_size(x_dtype);
+  bool vec_ok = (voxels % vec) == 0 && aligned_to(x, es * vec) && aligned_to(dx, es * vec);
+  if (soft && target)
+    vec_ok = vec_ok && (labels ? aligned_to(target, 16) : aligned_to(target, 4 * vec));
+
+  BwdParams p{};
+  p.x = x;
+  p.tgt = target;
+  p.dx = dx;
+  p.N = voxels;
+  p.tile_vox = g.tile_vox;
+  p.tiles = g.tiles;
+  p.B = (int)batch;
+  p.C = (int)channels;
+  p.off = g.off;
+  p.K = num_bins;
+  p.act = act;
+  p.tk = labels ? kTgtLabels : kTgtOnehot;
+  p.vec_ok = vec_ok ? 1 : 0;
+  p.go_per_class = grad_output_per_class != 0;
+  p.btab = bin_table;
+  p.rtab = centre_table;
+  p.coef = coef;
+  p.d = diff;
+  p.jac = jac;
+  p.go = grad_output;
+
+  return p;
+}
+
+// Bytes of one level's workspace region in a multi-level call.
+size_t level_ws_bytes(int64_t batch, int64_t channels, int64_t voxels, int num_bins, int binning,
+                      int include_background) {
+  const Geometry g = workspace_geometry(batch, channels, voxels, num_bins, binning,
+                                        include_background, ACE_TARGET_LABELS_I64);
+  const Geometry h = make_geometry(batch, channels, voxels, num_bins, binning == ACE_SOFT,
+                                   include_background != 0, true, env_steps("ACE_FWD_STEPS"),
+                                   env_copies());
+  return align_up(g.ws_bytes > h.ws_bytes ? g.ws_bytes : h.ws_bytes, 256);
+}
+
+template <typename T>
+hipError_t pick_levels_fwd(bool soft, bool right, int cmax, long long nblk, size_t lds,
+                           const FwdLevels& L, hipStream_t s) {
+  if (soft)
+    return right ? launch_levels_fwd<T, true, true>(cmax, nblk, lds, L, s)
+                 : launch_levels_fwd<T, true, false>(cmax, nblk, lds, L, s);
+  return right ? launch_levels_fwd<T, false, true>(cmax, nblk, lds, L, s)
+               : launch_levels_fwd<T, false, false>(cmax, nblk, lds, L, s);
+}
+template <typename T>
+hipError_t pick_levels_bwd(bool soft, bool right, int cmax, long long nblk, size_t lds,
+                           const BwdLevels& L, hipStream_t s) {
+  if (soft)
+    return right ? launch_levels_bwd<T, true, true>(cmax, nblk, lds, L, s)
+                 : launch_levels_bwd<T, true, false>(cmax, nblk, lds, L, s);
+  return right ? launch_levels_bwd<T, false, true>(cmax, nblk, lds, L, s)
+               : launch_levels_bwd<T, false, false>(cmax, nblk, lds, L, s);
+}
+
 }  // namespace
 }  // namespace ace
 
@@ -144,7 +273,7 @@ using namespace ace;
 
 extern "C" {
 
-int ace_abi_version(void) { return 3; }
+int ace_abi_version(void) { return 4; }
 
 const char* ace_error_string(int code) {
   switch (code) {
@@ -204,54 +333,10 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   if (g.lds_fwd > kMaxLds) return ACE_EUNSUPPORTED;
   if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
 
-  const int vec = g.var.vec;
-  const size_t es = elem_size(x_dtype);
-  const bool vec_ok = (voxels % vec) == 0 && aligned_to(x, es * vec) &&
-                      (labels ? aligned_to(target, 16) : aligned_to(target, 4 * vec));
-
-  FwdParams p{};
-  p.x = x;
-  p.tgt = target;
-  p.N = voxels;
-  p.tile_vox = g.tile_vox;
-  p.tiles = g.tiles;
-  p.gs = g.gs;
-  p.gpb = g.gpb;
-  p.B = (int)batch;
-  p.C = (int)channels;
-  p.off = g.off;
-  p.K = num_bins;
-  p.act = act;
-  p.tk = labels ? kTgtLabels : kTgtOnehot;
-  p.copies = g.copies;
-  p.vec_ok = vec_ok ? 1 : 0;
-  p.ignore_empty = ignore_empty_classes != 0;
-  p.red = reduction;
-  p.empty_w = empty_weight;
-  if (moments) {
-    const MomentScale ms = moment_scale(num_bins);
-    p.msc = ldexpf(1.0f, ms.m);
-    p.misc = ldexpf(1.0f, -ms.m);
-    p.mw = ms.w;
-    p.mshift = moment_shift(voxels);
-  }
-  p.btab = bin_table;
-  p.rtab = centre_table;
-  p.clsw = class_weight;
-  unsigned char* ws = static_cast<unsigned char*>(workspace);
-  p.ctr = reinterpret_cast<int*>(ws);
-  p.part = reinterpret_cast<unsigned long long*>(ws + g.off_part);
-  p.fin = reinterpret_cast<unsigned long long*>(ws + g.off_fin);
-  p.reps = g.reps;
-  p.lchunk = g.lchunk;
-  p.epi_all = g.epi_all ? 1 : 0;
-  p.coef = coef;
-  p.d = diff;
-  p.jac = jac;
-  p.f = per_class;
-  p.loss = loss;
-  p.stats = stats;
-
+  const FwdParams p = fwd_params(x, x_dtype, target, labels, voxels, batch, channels, num_bins, act,
+                                  ignore_empty_classes, reduction, empty_weight, moments, class_weight,
+                                  bin_table, centre_table, workspace, g, coef, diff, jac, per_class,
+                                  loss, stats);
   return to_code(dispatch_fwd(x_dtype, soft, right != 0, g, p, static_cast<hipStream_t>(stream)));
 }
 
@@ -278,35 +363,124 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
   if (voxels == 0) return ACE_OK;
 
-  const int vec = g.var.vec;
-  const size_t es = elem_size(x_dtype);
-  bool vec_ok = (voxels % vec) == 0 && aligned_to(x, es * vec) && aligned_to(dx, es * vec);
-  if (soft && target)
-    vec_ok = vec_ok && (labels ? aligned_to(target, 16) : aligned_to(target, 4 * vec));
-
-  BwdParams p{};
-  p.x = x;
-  p.tgt = target;
-  p.dx = dx;
-  p.N = voxels;
-  p.tile_vox = g.tile_vox;
-  p.tiles = g.tiles;
-  p.B = (int)batch;
-  p.C = (int)channels;
-  p.off = g.off;
-  p.K = num_bins;
-  p.act = act;
-  p.tk = labels ? kTgtLabels : kTgtOnehot;
-  p.vec_ok = vec_ok ? 1 : 0;
-  p.go_per_class = grad_output_per_class != 0;
-  p.btab = bin_table;
-  p.rtab = centre_table;
-  p.coef = coef;
-  p.d = diff;
-  p.jac = jac;
-  p.go = grad_output;
-
+  const BwdParams p = bwd_params(x, x_dtype, target, labels, soft, voxels, batch, channels, num_bins,
+                                  act, bin_table, centre_table, coef, diff, jac, grad_output,
+                                  grad_output_per_class, dx, g);
   return to_code(dispatch_bwd(x_dtype, soft, right != 0, g, p, static_cast<hipStream_t>(stream)));
+}
+
+size_t ace_workspace_bytes_levels(int levels, const int64_t* voxels, int64_t batch,
+                                  int64_t channels, int num_bins, int binning, int x_dtype,
+                                  int include_background) {
+  (void)x_dtype;
+  if (levels < 1 || levels > kMaxLevels || !voxels || batch < 1 || channels < 1 || num_bins < 1)
+    return 0;
+  size_t total = 0;
+  for (int l = 0; l < levels; ++l) {
+    if (voxels[l] < 0) return 0;
+    total += level_ws_bytes(batch, channels, voxels[l], num_bins, binning, include_background);
+  }
+  return total;
+}
+
+int ace_forward_levels(int levels, const AceFwdLevel* lv, int x_dtype, int64_t batch,
+                       int64_t channels, int num_bins, int binning, int include_background,
+                       int ignore_empty_classes, int reduction, int right, float empty_weight,
+                       const float* class_weight, const float* bin_table,
+                       const float* centre_table, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  if (levels < 1 || levels > kMaxLevels || !lv || !workspace) return ACE_EINVAL;
+  if (reduction != ACE_RED_MEAN && reduction != ACE_RED_SUM && reduction != ACE_RED_NONE)
+    return ACE_EINVAL;
+  if (!fast_channels(channels)) return ACE_EUNSUPPORTED;
+  const bool soft = binning == ACE_SOFT;
+  FwdLevels L{};
+  L.n = levels;
+  long long nblk = 0;
+  size_t lds = 0, off = 0;
+  int cmax = 0;
+  for (int l = 0; l < levels; ++l) {
+    const AceFwdLevel& v = lv[l];
+    int rc = check_common(v.x, x_dtype, v.target, ACE_TARGET_LABELS_I64, batch, channels, v.voxels,
+                          num_bins, binning, ACE_ACT_SOFTMAX, bin_table, centre_table, true);
+    if (rc) return rc;
+    if (!v.coef || !v.diff || !v.jac || !v.per_class) return ACE_EINVAL;
+    if (reduction != ACE_RED_NONE && !v.loss) return ACE_EINVAL;
+    const bool moments = use_moments(soft, true, kActSoftmax, batch, channels, v.voxels, num_bins,
+                                     include_background);
+    if (soft && !moments) return ACE_EUNSUPPORTED;
+    const Geometry g = make_geometry(batch, channels, v.voxels, num_bins, soft,
+                                     include_background != 0, true, env_steps("ACE_FWD_STEPS"),
+                                     env_copies(), moments);
+    if (g.lds_fwd > kMaxLds) return ACE_EUNSUPPORTED;
+    if (nblk + g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
+    L.lv[l] = fwd_params(v.x, x_dtype, v.target, true, v.voxels, batch, channels, num_bins,
+                         kActSoftmax, ignore_empty_classes, reduction, empty_weight, moments,
+                         class_weight, bin_table, centre_table,
+                         static_cast<unsigned char*>(workspace) + off, g, v.coef, v.diff, v.jac,
+                         v.per_class, v.loss, nullptr);
+    L.start[l] = nblk;
+    nblk += g.nblk;
+    lds = g.lds_fwd > lds ? g.lds_fwd : lds;
+    cmax = g.var.cmax;
+    off += level_ws_bytes(batch, channels, v.voxels, num_bins, binning, include_background);
+  }
+  if (workspace_bytes < off) return ACE_EWORKSPACE;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (x_dtype) {
+    case ACE_F32: e = pick_levels_fwd<float>(soft, right != 0, cmax, nblk, lds, L, s); break;
+    case ACE_BF16: e = pick_levels_fwd<__hip_bfloat16>(soft, right != 0, cmax, nblk, lds, L, s); break;
+    default: e = pick_levels_fwd<__half>(soft, right != 0, cmax, nblk, lds, L, s); break;
+  }
+  return to_code(e);
+}
+
+int ace_backward_levels(int levels, const AceBwdLevel* lv, int x_dtype, int64_t batch,
+                        int64_t channels, int num_bins, int binning, int include_background,
+                        int right, int grad_output_per_class, const float* bin_table,
+                        const float* centre_table, void* stream) {
+  if (levels < 1 || levels > kMaxLevels || !lv) return ACE_EINVAL;
+  if (!fast_channels(channels)) return ACE_EUNSUPPORTED;
+  const bool soft = binning == ACE_SOFT;
+  BwdLevels L{};
+  L.n = levels;
+  long long nblk = 0;
+  size_t lds = 0;
+  int cmax = 0;
+  for (int l = 0; l < levels; ++l) {
+    const AceBwdLevel& v = lv[l];
+    int rc = check_common(v.x, x_dtype, v.target, ACE_TARGET_LABELS_I64, batch, channels, v.voxels,
+                          num_bins, binning, ACE_ACT_SOFTMAX, bin_table, centre_table, soft);
+    if (rc) return rc;
+    if (!v.coef || !v.jac || !v.grad_output || (!v.dx && v.voxels > 0)) return ACE_EINVAL;
+    if (soft && !v.diff) return ACE_EINVAL;
+    const bool moments = use_moments(soft, true, kActSoftmax, batch, channels, v.voxels, num_bins,
+                                     include_background);
+    if (soft && !moments) return ACE_EUNSUPPORTED;
+    const Geometry g = make_geometry(batch, channels, v.voxels, num_bins, soft,
+                                     include_background != 0, true, env_steps("ACE_BWD_STEPS"), 0,
+                                     moments);
+    if (g.lds_bwd > kMaxLds) return ACE_EUNSUPPORTED;
+    if (nblk + g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
+    L.lv[l] = bwd_params(v.x, x_dtype, v.target, true, soft, v.voxels, batch, channels, num_bins,
+                         kActSoftmax, bin_table, centre_table, v.coef, v.diff, v.jac,
+                         v.grad_output, grad_output_per_class, v.dx, g);
+    L.start[l] = nblk;
+    // a level with no voxels launches no blocks (ace_backward returns early)
+    nblk += v.voxels > 0 ? g.nblk : 0;
+    lds = g.lds_bwd > lds ? g.lds_bwd : lds;
+    cmax = g.var.cmax;
+  }
+  if (nblk == 0) return ACE_OK;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (x_dtype) {
+    case ACE_F32: e = pick_levels_bwd<float>(soft, right != 0, cmax, nblk, lds, L, s); break;
+    case ACE_BF16: e = pick_levels_bwd<__hip_bfloat16>(soft, right != 0, cmax, nblk, lds, L, s); break;
+    default: e = pick_levels_bwd<__half>(soft, right != 0, cmax, nblk, lds, L, s); break;
+  }
+  return to_code(e);
 }
 
 int ace_set_launch_events(void* start, void* stop) {

@@ -1548,8 +1548,8 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
 
 // SKIP0: channel 0 (background) is not in the loss (P.off == 1).
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
-__global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
-  extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t blk,
+                                              unsigned char* smem) {
   float* tabs = reinterpret_cast<float*>(smem);
   const int K = P.K;
   const int n = SOFT ? 2 * K : K;
@@ -1560,7 +1560,6 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
   const int lr = __builtin_ctz((unsigned)R);
   const int lsh = lr + 3;
   const int tid = threadIdx.x;
-  const int64_t blk = blockIdx.x;
   const int b = (int)(blk / P.tiles);
   const int64_t tile = blk - (int64_t)b * P.tiles;
 
@@ -1718,8 +1717,8 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
 }
 
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
-__global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
-  extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t blk,
+                                              unsigned char* smem) {
   float* tabs = reinterpret_cast<float*>(smem);
   const int K = P.K;
   const int n = SOFT ? 2 * K : K;
@@ -1727,7 +1726,6 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   const int CL = C - off;
   const int CK = CL * K;
   const int tid = threadIdx.x;
-  const int64_t blk = blockIdx.x;
   const int b = (int)(blk / P.tiles);
   const int64_t tile = blk - (int64_t)b * P.tiles;
 
@@ -1839,12 +1837,67 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
   }
 }
 
+// One problem per launch: block blockIdx.x of P's grid.
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
+__global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  fwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(P, blockIdx.x, smem);
+}
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
+__global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  bwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(P, blockIdx.x, smem);
+}
+
+// Several problems of one configuration in one launch (the levels of a
+// deep-supervision step): problem l owns blocks [start[l], start[l + 1]) of
+// the grid and runs exactly as its own launch would, with its own workspace
+// region, so each result is bit-identical to a separate call.
+constexpr int kMaxLevels = 4;
+struct FwdLevels {
+  FwdParams lv[kMaxLevels];
+  long long start[kMaxLevels];  // first block of each level, increasing
+  int n;
+};
+struct BwdLevels {
+  BwdParams lv[kMaxLevels];
+  long long start[kMaxLevels];
+  int n;
+};
+__device__ __forceinline__ int level_of(const long long (&start)[kMaxLevels], int n, long long g) {
+  int l = 0;
+#pragma unroll
+  for (int j = 1; j < kMaxLevels; ++j)
+    if (j < n && g >= start[j]) l = j;
+  return l;
+}
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
+__global__ void __launch_bounds__(kThreads) fwd_kernel_fast_levels(const FwdLevels L) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const long long g = blockIdx.x;
+  const int l = level_of(L.start, L.n, g);
+  fwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(L.lv[l], g - L.start[l], smem);
+}
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
+__global__ void __launch_bounds__(kThreads) bwd_kernel_fast_levels(const BwdLevels L) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const long long g = blockIdx.x;
+  const int l = level_of(L.start, L.n, g);
+  bwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(L.lv[l], g - L.start[l], smem);
+}
+
 // ------------------------------------------------------------ launchers
 
 template <typename T, bool SOFT, bool RIGHT>
 hipError_t launch_variant_fwd(const Geometry& g, const FwdParams& prm, hipStream_t s);
 template <typename T, bool SOFT, bool RIGHT>
 hipError_t launch_variant_bwd(const Geometry& g, const BwdParams& prm, hipStream_t s);
+template <typename T, bool SOFT, bool RIGHT>
+hipError_t launch_levels_fwd(int cmax, long long nblk, size_t lds, const FwdLevels& L,
+                             hipStream_t s);
+template <typename T, bool SOFT, bool RIGHT>
+hipError_t launch_levels_bwd(int cmax, long long nblk, size_t lds, const BwdLevels& L,
+                             hipStream_t s);
 
 // The fast kernels serve softmax with class-index targets for C in {2, 3, 4, 16};
 // soft binning only in the moments layout (g.moments: the host declines it
@@ -1914,6 +1967,41 @@ hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) 
   return launch(kern, g.nblk, g.lds_bwd, s, prm);
 }
 
+// Multi-level launches: the fast kernels only (softmax, class-index
+// targets, C in {2, 3, 4, 16}, soft in the moments layout); every level
+// has the same configuration, so one instantiation serves all of them.
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT>
+hipError_t launch_fwd_levels_t(long long nblk, size_t lds, const FwdLevels& L, hipStream_t s) {
+  auto kern = L.lv[0].off ? fwd_kernel_fast_levels<T, C, VEC, SOFT, RIGHT, true>
+                          : fwd_kernel_fast_levels<T, C, VEC, SOFT, RIGHT, false>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  return launch(kern, nblk, lds, s, L);
+}
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT>
+hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, hipStream_t s) {
+  auto kern = L.lv[0].off ? bwd_kernel_fast_levels<T, C, VEC, SOFT, RIGHT, true>
+                          : bwd_kernel_fast_levels<T, C, VEC, SOFT, RIGHT, false>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  return launch(kern, nblk, lds, s, L);
+}
+
+#define ACE_LEVELS_SWITCH(LAUNCH, T, SOFT, RIGHT)                 \
+  switch (cmax) {                                                 \
+    case 2: return LAUNCH<T, 2, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
+    case 3: return LAUNCH<T, 3, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
+    case 4: return LAUNCH<T, 4, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
+    case 16: return LAUNCH<T, 16, 2, SOFT, RIGHT>(nblk, lds, L, s); \
+  }                                                               \
+  return hipErrorInvalidValue;
+
 // Instantiates the per-variant switch for one (element type, binning, right).
 #define ACE_VARIANT_SWITCH(LAUNCH, T, SOFT, RIGHT)                                   \
   const Variant v = g.var;                                                           \
@@ -1945,6 +2033,16 @@ hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) 
   hipError_t launch_variant_bwd<T, SOFT, RIGHT>(const Geometry& g, const BwdParams& p, \
                                                 hipStream_t s) {                     \
     ACE_VARIANT_SWITCH(launch_bwd_t, T, SOFT, RIGHT)                                 \
+  }                                                                                  \
+  template <>                                                                        \
+  hipError_t launch_levels_fwd<T, SOFT, RIGHT>(int cmax, long long nblk, size_t lds,   \
+                                               const FwdLevels& L, hipStream_t s) {  \
+    ACE_LEVELS_SWITCH(launch_fwd_levels_t, T, SOFT, RIGHT)                           \
+  }                                                                                  \
+  template <>                                                                        \
+  hipError_t launch_levels_bwd<T, SOFT, RIGHT>(int cmax, long long nblk, size_t lds,   \
+                                               const BwdLevels& L, hipStream_t s) {  \
+    ACE_LEVELS_SWITCH(launch_bwd_levels_t, T, SOFT, RIGHT)                           \
   }
 
 }  // namespace ace

@@ -127,6 +127,57 @@ int ace_backward(const void* x, int x_dtype, const void* target,
                  void* dx, void* stream);
 
 /*
+ * Several levels of one loss in one launch per direction (deep supervision:
+ * the same configuration on up to 4 resolutions of one batch).  No
+ * counterpart in the reference, whose API takes one volume per call
+ * (src/ace_kernels/registry.py:78-100) and which runs one call per level
+ * (bench/configs/sprint11_deepsup.yaml).  Each level's outputs are
+ * bit-identical to those of ace_forward / ace_backward on that level alone;
+ * the launch saves the per-call latency of the small levels.  Only the
+ * configurations with a fast kernel: softmax, int64 class-index targets,
+ * C in {2, 3, 4, 16}, soft binning within the moments limits (else
+ * ACE_EUNSUPPORTED).  The workspace holds one region per level, in order.
+ */
+typedef struct AceFwdLevel {
+  const void* x;          /* [B, C, voxels] logits                  */
+  const void* target;     /* [B, voxels] int64 class ids            */
+  int64_t voxels;
+  float* coef;            /* outputs as ace_forward                 */
+  float* diff;
+  float* jac;
+  float* per_class;
+  float* loss;
+} AceFwdLevel;
+
+typedef struct AceBwdLevel {
+  const void* x;
+  const void* target;     /* may be NULL for hard binning           */
+  int64_t voxels;
+  const float* coef;      /* that level's forward outputs           */
+  const float* diff;
+  const float* jac;
+  const float* grad_output;
+  void* dx;
+} AceBwdLevel;
+
+size_t ace_workspace_bytes_levels(int levels, const int64_t* voxels,
+                                  int64_t batch, int64_t channels,
+                                  int num_bins, int binning, int x_dtype,
+                                  int include_background);
+int ace_forward_levels(int levels, const AceFwdLevel* lv, int x_dtype,
+                       int64_t batch, int64_t channels, int num_bins,
+                       int binning, int include_background,
+                       int ignore_empty_classes, int reduction, int right,
+                       float empty_weight, const float* class_weight,
+                       const float* bin_table, const float* centre_table,
+                       void* workspace, size_t workspace_bytes, void* stream);
+int ace_backward_levels(int levels, const AceBwdLevel* lv, int x_dtype,
+                        int64_t batch, int64_t channels, int num_bins,
+                        int binning, int include_background, int right,
+                        int grad_output_per_class, const float* bin_table,
+                        const float* centre_table, void* stream);
+
+/*
  * Kernel timing.  This has no counterpart in the reference, whose benchmark
  * brackets each call with events recorded on the stream
  * (src/ace_bench/timing.py:48-77); on HIP such events also time the dispatch

@@ -1,0 +1,96 @@
+"""Several levels of one loss in one launch per direction (``ace_loss_levels``):
+each level's loss and gradient are bit-identical to a separate
+``ace_loss(..., impl="hip_mi355x")`` call on that level (same blocks, same
+integer sums), for hard and soft binning, every fast channel count,
+background dropped, the three reductions, per-class upstream gradients, an
+empty level, and configurations without a fast kernel rejected."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from ace_kernels import ACEConfig, ace_loss
+from ace_kernels.levels import ace_loss_levels
+from gpu_helpers import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _levels(b, c, sizes, seed):
+    gen = torch.Generator().manual_seed(seed)
+    xs, ys = [], []
+    for s in sizes:
+        shape = (b, c, *s)
+        xs.append((torch.randn(shape, generator=gen) * 2.0).cuda())
+        ys.append(torch.randint(0, c, (b, 1, *s), generator=gen).cuda())
+    return xs, ys
+
+
+def _separate(xs, ys, cfg, ups):
+    out = []
+    for x, y, up in zip(xs, ys, ups):
+        leaf = x.clone().requires_grad_(True)
+        loss = ace_loss(leaf, y, cfg, impl="hip_mi355x")
+        (g,) = torch.autograd.grad(loss, leaf, up.view_as(loss))
+        out.append((loss.detach(), g))
+    return out
+
+
+def _together(xs, ys, cfg, ups):
+    leaves = [x.clone().requires_grad_(True) for x in xs]
+    losses = ace_loss_levels(leaves, ys, cfg)
+    grads = torch.autograd.grad(losses, leaves, [u.view_as(l) for u, l in zip(ups, losses)])
+    return [(l.detach(), g) for l, g in zip(losses, grads)]
+
+
+SIZES = [(32, 32, 32), (16, 16, 16), (8, 8, 8), (4, 4, 4)]
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+@pytest.mark.parametrize("c,kw", [
+    (4, {}),
+    (4, {"reduction": "sum"}),
+    (4, {"reduction": "none", "include_background": False}),
+    (2, {"num_bins": 7, "right": True}),
+    (3, {"weight": [0.5, 2.0, 1.0]}),
+    (16, {}),
+])
+def test_levels_match_separate_calls(binning, c, kw) -> None:
+    cfg = ACEConfig(binning=binning, to_onehot_y=True, activation="softmax", **kw)
+    xs, ys = _levels(2, c, SIZES, seed=51 + c)
+    cl = c - (0 if cfg.include_background else 1)
+    gen = torch.Generator().manual_seed(7)
+    ups = [torch.rand((2, cl) if cfg.reduction == "none" else (), generator=gen).cuda() + 0.5
+           for _ in SIZES]
+    say(f"levels {binning} C={c} {kw}")
+    want = _separate(xs, ys, cfg, ups)
+    got = _together(xs, ys, cfg, ups)
+    for (lw, gw), (lg, gg) in zip(want, got):
+        assert torch.equal(lg, lw)
+        assert torch.equal(gg, gw)
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_levels_with_an_empty_level_and_two_levels(binning) -> None:
+    cfg = ACEConfig(binning=binning, to_onehot_y=True, activation="softmax")
+    for sizes in ([(24, 20, 16), (0, 5)], [(9, 7, 5)]):
+        xs, ys = _levels(3, 4, sizes, seed=61)
+        ups = [torch.ones(()).cuda() for _ in sizes]
+        say(f"levels {binning} {sizes}")
+        want = _separate(xs, ys, cfg, ups)
+        got = _together(xs, ys, cfg, ups)
+        for (lw, gw), (lg, gg) in zip(want, got):
+            torch.testing.assert_close(lg, lw, rtol=0, atol=0, equal_nan=True)
+            assert torch.equal(gg, gw)
+
+
+def test_levels_reject_configurations_without_a_fast_kernel() -> None:
+    xs, ys = _levels(2, 5, [(8, 8, 8), (4, 4, 4)], seed=3)
+    cfg = ACEConfig(binning="hard", to_onehot_y=True, activation="softmax")
+    say("levels: C=5 rejected")
+    with pytest.raises(Exception, match="unsupported"):
+        ace_loss_levels(xs, ys, cfg)
+    xs, ys = _levels(2, 4, [(8, 8, 8)], seed=3)
+    with pytest.raises(ValueError):
+        ace_loss_levels(xs, ys, ACEConfig(binning="hard", to_onehot_y=True, activation="sigmoid"))
