@@ -236,7 +236,8 @@ def bench_workload(wl, steps: int, warmup: int, flush):
 def bench_deep_supervision(binning: str, steps: int, warmup: int, flush):
     """Deep-supervision step: one loss call per level (128^3 ... 16^3, B=1) and
     one backward through the sum of the four losses; eager and HIP-graph
-    replay, plus each level's own fwd+bwd step."""
+    replay; the same step with all levels in one launch per direction
+    (``ace_loss_levels``); and each level's own fwd+bwd step."""
     import torch
 
     from ace_kernels import ace_loss
@@ -271,6 +272,30 @@ def bench_deep_supervision(binning: str, steps: int, warmup: int, flush):
     graph_ok = all(bool(torch.equal(a, b)) for a, b in zip(g_static, g_eager))
     graphed = time_steps(graph.replay, steps, warmup, flush)
     del graph
+    # the same step with every level in one launch per direction
+    from ace_kernels.levels import ace_loss_levels
+
+    ys = [d[1] for d in data]
+    cfg0 = data[0][2]
+
+    def step_levels():
+        total = sum(ace_loss_levels(xs, ys, cfg0))
+        return torch.autograd.grad(total, xs)
+
+    lv_eager = time_steps(step_levels, steps, warmup, flush)
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step_levels()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        lv_static = step_levels()
+    graph.replay()
+    torch.cuda.synchronize()
+    lv_ok = all(bool(torch.equal(a, b)) for a, b in zip(lv_static, g_eager))
+    lv_graphed = time_steps(graph.replay, steps, warmup, flush)
+    del graph
     per_level = {}
     for wl, (x, y, cfg) in zip(levels, data):
         def one(x=x, y=y, cfg=cfg):
@@ -284,6 +309,9 @@ def bench_deep_supervision(binning: str, steps: int, warmup: int, flush):
         "eager_ms": _quantiles(eager),
         "graph_ms": _quantiles(graphed),
         "graph_replay_matches_eager": graph_ok,
+        "one_launch_eager_ms": _quantiles(lv_eager),
+        "one_launch_graph_ms": _quantiles(lv_graphed),
+        "one_launch_matches_per_level_calls": lv_ok,
         "level_eager_ms_p50": per_level,
         "pct_hbm_peak": 100.0 * ideal / (_quantiles(eager)["p50"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
     }
