@@ -71,3 +71,30 @@ def test_missing_library_fails_loudly(monkeypatch: pytest.MonkeyPatch, tmp_path:
     finally:
         monkeypatch.undo()
         _lib.lib.cache_clear()
+
+
+def test_level_entry_points_validate_before_launch() -> None:
+    """ace_forward_levels / ace_backward_levels reject bad level counts, null
+    per-level pointers and configurations without a fast kernel before any
+    HIP call (none of these reach the GPU)."""
+    import ctypes
+
+    lib = _lib.lib()
+    vox = (ctypes.c_int64 * 2)(4096, 512)
+    one = lib.ace_workspace_bytes_levels(1, vox, 2, 4, 20, _lib.HARD, _lib.F32, 1)
+    two = lib.ace_workspace_bytes_levels(2, vox, 2, 4, 20, _lib.HARD, _lib.F32, 1)
+    assert 0 < one < two and one % 256 == 0 and two % 256 == 0
+    assert lib.ace_workspace_bytes_levels(0, vox, 2, 4, 20, _lib.HARD, _lib.F32, 1) == 0
+    assert lib.ace_workspace_bytes_levels(5, vox, 2, 4, 20, _lib.HARD, _lib.F32, 1) == 0
+    fwd = (_lib.AceFwdLevel * 2)()
+    common = [_lib.F32, 2, 4, 20, _lib.HARD, 1, 1, _lib.RED_MEAN, 0, 0.01, None, None, None]
+    assert lib.ace_forward_levels(0, fwd, *common, None, 0, None) == 1      # no levels
+    assert lib.ace_forward_levels(5, fwd, *common, None, 0, None) == 1      # above the maximum
+    assert lib.ace_forward_levels(2, fwd, *common, None, 0, None) == 1      # null workspace
+    c5 = [_lib.F32, 2, 5, 20, _lib.HARD, 1, 1, _lib.RED_MEAN, 0, 0.01, None, None, None]
+    assert lib.ace_forward_levels(2, fwd, *c5, 1, 1 << 20, None) == 2      # C = 5: no fast kernel
+    bwd = (_lib.AceBwdLevel * 2)()
+    assert lib.ace_backward_levels(0, bwd, _lib.F32, 2, 4, 20, _lib.HARD, 1, 0, 0, None, None,
+                                   None) == 1
+    assert lib.ace_backward_levels(2, bwd, _lib.F32, 2, 16, 20, _lib.HARD, 1, 0, 0, None, None,
+                                   None) == 1                              # null bin table
