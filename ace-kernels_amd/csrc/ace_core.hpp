@@ -1546,7 +1546,8 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
   }
 }
 
-// SKIP0: channel 0 (background) is not in the loss (P.off == 1).
+// SKIP0: channel 0 (background) is not in the loss (P.off == 1).  blk is the
+// block's index in P's own grid, smem the block's dynamic LDS.
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
 __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t blk,
                                               unsigned char* smem) {
