@@ -117,9 +117,8 @@ def _stream(dev: torch.device) -> int:
 
 
 @lru_cache(maxsize=256)
-def _workspace_sizes(dims: Tuple[int, ...]) -> Tuple[int, int]:
-    lib = _lib.lib()
-    return lib.ace_workspace_bytes(*dims), lib.ace_workspace_reset_bytes(*dims)
+def _workspace_bytes(dims: Tuple[int, ...]) -> int:
+    return _lib.lib().ace_workspace_bytes(*dims)
 
 
 def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False, shared: bool = True):
@@ -132,7 +131,7 @@ def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False, shared: bool =
     stream = _stream(dev)
     binning = _lib.SOFT if pl.soft else _lib.HARD
     dims = (pl.B, pl.C, pl.N, pl.K, binning, pl.dtype_code, int(pl.include_bg), pl.target_kind)
-    ws = workspace(dev, stream, *_workspace_sizes(dims))
+    ws = workspace(dev, stream, _workspace_bytes(dims))
     f32 = torch.float32
     # coef, d and jac (all saved for backward) share one allocation; the
     # per-class errors and the loss, which the caller may receive and modify

@@ -52,7 +52,7 @@ def forward_levels(plans: Sequence[Plan], config: ACEConfig):
     vox = (ctypes.c_int64 * n)(*[p.N for p in plans])
     nbytes = lib.ace_workspace_bytes_levels(n, vox, p0.B, p0.C, p0.K, binning, p0.dtype_code,
                                             int(p0.include_bg))
-    ws = workspace(dev, stream, nbytes, nbytes)
+    ws = workspace(dev, stream, nbytes)
     reduction = _REDUCTIONS[config.reduction]
     f32 = torch.float32
     bck, bc = p0.B * p0.CL * p0.K, p0.B * p0.CL

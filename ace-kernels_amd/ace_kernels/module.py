@@ -40,15 +40,17 @@ def _reduction(reduction) -> str:
     return value
 
 
-def _weight(weight: Weight) -> Union[Tuple[float, ...], float, None]:
-    if weight is None:
-        return None
+def _config_weight(weight: Weight) -> Union[Tuple[float, ...], float, None]:
+    """``weight`` as the plain floats ``ACEConfig.weight`` holds: a 0-d tensor
+    or a number becomes one float, a tensor or sequence a tuple of floats."""
     if isinstance(weight, torch.Tensor):
-        values = [float(w) for w in weight.flatten().tolist()]
-        return values[0] if weight.dim() == 0 else tuple(values)
-    if isinstance(weight, (int, float)):
+        flat = [float(v) for v in weight.detach().reshape(-1).tolist()]
+        return flat[0] if weight.dim() == 0 else tuple(flat)
+    if weight is None or isinstance(weight, float):
+        return weight
+    if isinstance(weight, int):
         return float(weight)
-    return tuple(float(w) for w in weight)
+    return tuple(map(float, weight))
 
 
 class _ACELoss(torch.nn.modules.loss._Loss):
@@ -89,16 +91,17 @@ class _ACELoss(torch.nn.modules.loss._Loss):
             include_background=include_background,
             ignore_empty_classes=ignore_empty_classes,
             reduction=red,
-            weight=_weight(weight),
+            weight=_config_weight(weight),
             right=right,
             empty_weight=empty_weight,
         )
         self.config_json = self.config.model_dump_json()
         if impl != "auto":
-            get_impl(impl)  # fail early on an unknown name
+            get_impl(impl)  # an unknown name raises KeyError here, at construction
 
     def resolve_impl(self, device: torch.device) -> str:
-        """Implementation used for inputs on ``device``."""
+        """The registry name this module calls for tensors on ``device``:
+        its fixed ``impl``, or with ``"auto"`` the HIP kernels for HIP tensors."""
         if self.impl != "auto":
             return self.impl
         if device.type == "cuda":
@@ -109,9 +112,10 @@ class _ACELoss(torch.nn.modules.loss._Loss):
         )
 
     def forward(self, input: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
-        """``input``: logits ``[B, C, *spatial]`` (probabilities when no
-        activation); ``target``: one-hot ``[B, C, ...]`` or class indices
-        ``[B, 1, ...]`` with ``to_onehot_y``."""
+        """Loss of ``input`` (``[B, C, *spatial]`` logits, or probabilities
+        when no activation is set) against ``target`` (class ids
+        ``[B, 1, *spatial]`` when ``to_onehot_y``, else per-channel targets
+        ``[B, C, *spatial]``)."""
         if self.other_act is not None:
             input = self.other_act(input)
         name = self.resolve_impl(input.device)
@@ -132,7 +136,8 @@ class _ACELoss(torch.nn.modules.loss._Loss):
 
 
 class HardL1ACELoss(_ACELoss):
-    """Hard-binned L1 average calibration error (mL1-ACE); upstream signature."""
+    """mL1-ACE with hard binning: each probability counts in the one bin that
+    holds it.  Constructor arguments as the upstream class."""
 
     binning = "hard"
 
@@ -160,7 +165,7 @@ class HardL1ACELoss(_ACELoss):
             other_act=other_act,
             reduction=reduction,
             weight=weight,
-            empty_weight=0.01,  # unused by hard binning
+            empty_weight=0.01,  # the config's default; hard binning never reads it
             right=right,
             ignore_empty_classes=ignore_empty_classes,
             impl=impl,
@@ -168,7 +173,8 @@ class HardL1ACELoss(_ACELoss):
 
 
 class SoftL1ACELoss(_ACELoss):
-    """Soft-binned L1 average calibration error (mL1-ACE); upstream signature."""
+    """mL1-ACE with soft binning: each probability is split between the two
+    nearest bin centres.  Constructor arguments as the upstream class."""
 
     binning = "soft"
 

@@ -27,7 +27,8 @@ ALL_DEVICES: FrozenSet[str] = frozenset({"cpu", "cuda"})
 
 @dataclass(frozen=True)
 class ImplSpec:
-    """A registered implementation and the settings it supports."""
+    """One registry entry: the loss function under ``name``, the binnings and
+    device types it accepts, a one-line description, and whether it is slow."""
 
     name: str
     fn: ACEFn
@@ -51,7 +52,8 @@ def register(
     devices: FrozenSet[str] = ALL_DEVICES,
     slow: bool = False,
 ) -> Callable[[ACEFn], ACEFn]:
-    """Decorator adding an implementation to the registry under ``name``."""
+    """Returns a decorator that files ``fn`` under ``name`` (``ValueError`` if
+    the name is taken) and hands ``fn`` back unchanged."""
 
     def decorator(fn: ACEFn) -> ACEFn:
         if name in _REGISTRY:
@@ -74,7 +76,8 @@ def get_impl(name: str) -> ImplSpec:
 def available_impls(
     binning: Optional[Binning] = None, device: Optional[str] = None
 ) -> List[ImplSpec]:
-    """Registered implementations, optionally filtered by binning and device."""
+    """Every registry entry, or only those accepting ``binning`` and/or
+    ``device`` when given, in registration order."""
     return [
         spec
         for spec in _REGISTRY.values()
@@ -83,28 +86,46 @@ def available_impls(
     ]
 
 
+def resolve_impl(impl: str, binning: str, device_type: str) -> str:
+    """``impl`` itself, or for ``"auto"``: the HIP kernels (``hip_mi355x``) for
+    HIP tensors, else the first registered entry accepting ``binning`` on
+    ``device_type`` (this package registers none for the CPU)."""
+    if impl != "auto":
+        return impl
+    if device_type == "cuda" and "hip_mi355x" in _REGISTRY:
+        return "hip_mi355x"
+    for spec in _REGISTRY.values():
+        if spec.supports(binning, device_type):
+            return spec.name
+    raise ValueError(
+        f"no registered implementation accepts binning={binning!r} on {device_type!r} tensors "
+        "(this package computes on HIP devices; pass tensors on 'cuda')"
+    )
+
+
 def ace_loss(
     input: torch.Tensor,
     target: torch.Tensor,
     config: Optional[ACEConfig] = None,
-    impl: str = "reference",
+    impl: str = "auto",
 ) -> torch.Tensor:
-    """Compute the mL1-ACE loss with the chosen implementation.
+    """The mL1-ACE loss of ``input`` against ``target`` from registry entry ``impl``.
 
-    Args:
-        input: logits or probabilities, shape ``[B, C, *spatial]``.
-        target: one-hot ``[B, C, *spatial]``, or labels ``[B, 1, *spatial]``
-            when ``config.to_onehot_y`` is set.
-        config: loss options; defaults to ``ACEConfig()``.
-        impl: registered implementation name. This package registers
-            ``"hip_mi355x"``; ``"reference"`` exists only where a CPU reference
-            implementation has been registered (the test suite does so).
+    ``input`` holds ``[B, C, *spatial]`` logits (probabilities when
+    ``config.activation`` is "none"); ``target`` holds class ids
+    ``[B, 1, *spatial]`` when ``config.to_onehot_y`` is set, per-channel
+    targets ``[B, C, *spatial]`` otherwise.  ``config`` defaults to
+    ``ACEConfig()``.  ``impl="auto"`` picks ``hip_mi355x`` for HIP tensors
+    (``resolve_impl``); any registered name can be given instead.  The
+    reference's default name, ``"reference"``, exists only where a CPU
+    reference has been registered (the test suite registers its oracle).
     """
     config = config if config is not None else ACEConfig()
-    spec = get_impl(impl)
+    name = resolve_impl(impl, config.binning, input.device.type)
+    spec = get_impl(name)
     if not spec.supports(config.binning, input.device.type):
         raise ValueError(
-            f"{impl!r} does not support binning={config.binning!r} "
+            f"{name!r} does not support binning={config.binning!r} "
             f"on device={input.device.type!r}"
         )
     return spec.fn(input, target, config)

@@ -89,3 +89,31 @@ def test_tables_are_the_reference_linspace() -> None:
         assert torch.equal(half, full[1:])
         assert repl.numel() == 2 * k + 2 and repl[0] == -1e4 and repl[-1] == 1e4
         assert torch.equal(repl[1:-1:2], full[1::2]) and torch.equal(repl[2:-1:2], full[1::2])
+
+
+def test_default_impl_resolves_automatically() -> None:
+    """``ace_loss(x, y, config)`` with no impl: HIP tensors take hip_mi355x;
+    CPU tensors take the first registered CPU entry (the test suite's oracle),
+    and with none registered the call raises a clear ValueError."""
+    from ace_kernels.registry import resolve_impl
+
+    assert resolve_impl("auto", "hard", "cuda") == "hip_mi355x"
+    assert resolve_impl("auto", "soft", "cuda") == "hip_mi355x"
+    assert resolve_impl("hip_mi355x_op", "hard", "cuda") == "hip_mi355x_op"
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 3, 5, 4, generator=gen)
+    y = torch.randint(0, 3, (2, 1, 5, 4), generator=gen)
+    cfg = ACEConfig(to_onehot_y=True, activation="softmax")
+    cpu_name = resolve_impl("auto", "hard", "cpu")
+    assert get_impl(cpu_name).supports("hard", "cpu")
+    assert torch.equal(ace_loss(x, y, cfg), ace_loss(x, y, cfg, impl=cpu_name))
+
+
+def test_default_impl_without_a_cpu_entry_raises(monkeypatch: pytest.MonkeyPatch) -> None:
+    from ace_kernels import registry
+
+    kept = {k: v for k, v in registry._REGISTRY.items() if "cpu" not in v.devices}
+    monkeypatch.setattr(registry, "_REGISTRY", kept)
+    x = torch.rand(1, 2, 4)
+    with pytest.raises(ValueError, match="no registered implementation"):
+        ace_loss(x, x, ACEConfig())
