@@ -16,11 +16,11 @@
 Every cached device buffer lives until the process ends.  A HIP graph keeps
 the raw addresses it captured, so nothing a capture may have used is ever
 freed: a table or class-weight tensor is never evicted, and a workspace that
-a larger problem outgrows is retired (kept) rather than released.  Building
-any of them needs an allocation or a host-to-device copy, which a stream
-capture cannot record, so the first call of a new (K, device), class-weight
-set, or larger workspace size on a stream must run before capture; inside a
-capture such a call raises ``RuntimeError``.
+a larger problem outgrows is retired (kept) rather than released.  Tables
+and class weights are copied from the host, which a stream capture cannot
+record, so the first call of a new (K, device) or class-weight set must run
+before capture (inside a capture it raises ``RuntimeError``); a workspace a
+capture lacks is made for that capture alone (``workspace``).
 """
 
 from __future__ import annotations
@@ -134,13 +134,22 @@ def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     replays only.  A graph's replays share the capture stream's buffer with
     the eager calls made on that stream until it is replaced: order them
     (replay on the capture stream, or synchronise).
+
+    During a capture on a stream without a large enough buffer, the call gets
+    a buffer of its own: allocated from the capture's memory pool, zeroed by
+    a fill kernel that the graph records (so every replay starts from zero),
+    kept for the life of the process, and never handed to eager calls, whose
+    buffer must be zeroed when they run.
     """
     key = (*_device_key(device), int(stream))
     with _WS_LOCK:
         buf = _WORKSPACES.get(key)
         if buf is not None and buf.numel() >= nbytes:
             return buf
-        _refuse_under_capture(device, f"a workspace of {nbytes} bytes for this stream")
+        if capturing(device):
+            own = torch.zeros(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+            _RETIRED.append(own)
+            return own
         size = max(int(nbytes), 1 << 16, 2 * (buf.numel() if buf is not None else 0))
         new = torch.zeros(size, dtype=torch.uint8, device=device)
         if buf is not None:

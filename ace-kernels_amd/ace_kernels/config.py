@@ -9,6 +9,7 @@ from __future__ import annotations
 
 from typing import Literal, Optional, Tuple, Union
 
+import torch.utils._pytree
 from pydantic import BaseModel, ConfigDict, Field
 
 Binning = Literal["hard", "soft"]
@@ -45,3 +46,12 @@ class ACEConfig(BaseModel):
     weight: Optional[Union[Tuple[float, ...], float]] = None
     right: bool = False
     empty_weight: float = Field(default=0.01, ge=0.0)
+
+
+# torch.compile: an ACEConfig is a constant of the traced program (frozen,
+# hashable, compared by value), so `ace_loss(net(x), y, config, impl=...)`
+# traces with the config folded in, as the reference's compile test does
+# (tests/test_triton.py:474-495 upstream).  Without this, dynamo cannot pass
+# the pydantic object to the custom ops' constant JSON argument.
+if hasattr(torch.utils._pytree, "register_constant"):
+    torch.utils._pytree.register_constant(ACEConfig)

@@ -4,9 +4,10 @@ benchmark harness schema, for the implementations of this package.
 Mirrors ``src/ace_bench/measure.py`` (``Row`` :27-81, ``compute_reference``
 :142-186, ``_check_output`` :189-212, ``measure_case`` :280-360),
 ``src/ace_bench/calculator.py:23-44`` (ideal bytes and floors) and
-``src/ace_bench/timing.py:48-77`` (CUDA events, a 256 MiB write before each
-rep so the rep starts with a cold cache), so a row from this package can be
-put beside a row of the reference's harness:
+``src/ace_bench/timing.py:48-77`` (CUDA events, a cache flush before each
+rep so the rep starts with a cold cache: the reference writes 256 MiB, here
+1 GiB is read, more than MI355X's 256 MB last-level cache), so a row from
+this package can be put beside a row of the reference's harness:
 
 - timing: p50 / p20 / p80 / mean / std of ``reps`` event-timed calls;
 - bytes and floors: ideal bytes (fwd: x + target; fwd_bwd: 2 (x + target) +
@@ -45,7 +46,10 @@ Status = Literal["ok", "oom", "error", "unsupported", "capture_failed"]
 
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 LAUNCH_US = 5.0  # per-kernel launch floor (calculator.py:20-21)
-FLUSH_BYTES = 256 * 1024 * 1024  # timing.py:15
+# cold-cache flush: the reference writes 256 MiB (timing.py:15), sized for its
+# GPU's cache; MI355X has a 256 MB last-level cache, so here 1 GiB is read
+# (reads leave no dirty lines for the timed call to write back)
+FLUSH_BYTES = 1 << 30
 
 
 class Row(BaseModel):
@@ -181,21 +185,23 @@ def summarize(ms: List[float]) -> TimingStats:
 
 
 def measure(fn: Callable[[], object], warmup: int = 5, reps: int = 20, flush: bool = True) -> TimingStats:
-    """Event-timed calls of ``fn`` on the current stream, each after a 256 MiB
-    write (the reference's cold-cache method)."""
+    """Event-timed calls of ``fn`` on the current stream, each after a read of
+    FLUSH_BYTES (the reference's cold-cache method, sized for MI355X)."""
     for _ in range(warmup):
         fn()
-    buf = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
+    buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda")
+    sink = torch.empty((), dtype=torch.float32, device="cuda")
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     torch.cuda.synchronize()
     for s, e in zip(starts, ends):
         if flush:
-            buf.zero_()
+            torch.sum(buf, dim=0, out=sink)
         s.record()
         fn()
         e.record()
     torch.cuda.synchronize()
+    del buf
     return summarize([s.elapsed_time(e) for s, e in zip(starts, ends)])
 
 
@@ -298,7 +304,7 @@ def graphed(fn: Callable[[], object]) -> Callable[[], object]:
             fn()
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         fn()
     return graph.replay
 

@@ -54,8 +54,12 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm under /opt/rocm)")
 
 
-def _compile(src: Path, extra: list) -> Path:
+def _compile(src: Path, extra: list, incremental: bool = False) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
+    if incremental and obj.exists():
+        deps = [src, *CSRC.glob("*.hpp"), *INCLUDE.glob("*.h")]
+        if obj.stat().st_mtime > max(d.stat().st_mtime for d in deps):
+            return obj
     cmd = [hipcc(), *HIP_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -63,14 +67,15 @@ def _compile(src: Path, extra: list) -> Path:
     return obj
 
 
-def build(verbose: bool = False, extra: list | None = None) -> Path:
-    """Compile every csrc/*.hip and link ace_kernels/libace_hip.so; return its path."""
+def build(verbose: bool = False, extra: list | None = None, incremental: bool = False) -> Path:
+    """Compile every csrc/*.hip and link ace_kernels/libace_hip.so; return its path.
+    ``incremental``: skip objects newer than their source and every header."""
     extra = list(extra or [])
     OBJ_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(s, extra), sources))
+        objs = list(pool.map(lambda s: _compile(s, extra, incremental), sources))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -85,6 +90,8 @@ def build(verbose: bool = False, extra: list | None = None) -> Path:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--check", action="store_true", help="print register/LDS usage (-Rpass-analysis)")
+    ap.add_argument("--incremental", action="store_true",
+                    help="recompile only objects older than their source or a header")
     args = ap.parse_args()
     extra = ["-Rpass-analysis=kernel-resource-usage"] if args.check else []
     if args.check:
@@ -93,7 +100,7 @@ def main() -> int:
             cmd = [hipcc(), *HIP_FLAGS, *extra, "-c", str(src), "-o", str(OBJ_DIR / (src.stem + ".o"))]
             res = subprocess.run(cmd, capture_output=True, text=True)
             sys.stdout.write(res.stderr)
-    build(verbose=True)
+    build(verbose=True, incremental=args.incremental)
     return 0
 
 

@@ -120,25 +120,73 @@ int to_code(hipError_t e) { return e == hipSuccess ? ACE_OK : ACE_EHIP + (int)e;
 // moments' LDS layout (48 C'K bytes per copy, and the epilogue's terms)
 // allow it; otherwise the generic soft kernels (per-voxel weights, 24 C'K
 // bytes per copy).  Forward and backward take the same decision.
+// The test uses the 256-thread layout (at most 32 KB of copies); a
+// 1024-thread block then fits as well (fewer copies if need be, or 256
+// threads, make_geometry), so the decision does not depend on the block size.
 bool use_moments(bool soft, bool labels, int act, int64_t batch, int64_t channels, int64_t voxels,
                  int num_bins, int include_background) {
   if (!(soft && labels && act == kActSoftmax && fast_channels(channels) &&
         num_bins <= kMomentMaxBins))
     return false;
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, true, include_background != 0,
-                                   true, env_steps("ACE_FWD_STEPS"), env_copies(), true);
+                                   true, env_steps("ACE_FWD_STEPS"), env_copies(), true, true,
+                                   kThreads);
   return g.lds_fwd <= kMaxLds && g.lds_bwd <= kMaxLds;
 }
 
-// The activation is not an argument here: size for the larger layout (soft
-// moments when the channel count has a fast kernel and targets are labels).
-Geometry workspace_geometry(int64_t batch, int64_t channels, int64_t voxels, int num_bins,
-                            int binning, int include_background, int target_kind) {
+// The forward runs a fast kernel (fast_bins, 1024-thread blocks where the
+// histogram copies allow): softmax over a fast channel count with class
+// labels, soft binning in the moments layout.
+bool fast_forward(bool soft, bool labels, int act, int64_t channels, bool moments) {
+  return act == kActSoftmax && labels && fast_channels(channels) && (!soft || moments);
+}
+
+// Tuning knob for experiments: largest forward block size (256 or 1024).
+int env_max_threads() {
+  const char* v = getenv("ACE_FWD_MAX_THREADS");
+  return (v && atoi(v) == kThreads) ? kThreads : kFastThreads;
+}
+
+// Forward geometry of one problem (the kernel the launcher will pick).
+Geometry forward_geometry(int64_t batch, int64_t channels, int64_t voxels, int num_bins, bool soft,
+                          int include_background, bool labels, int act, bool moments,
+                          int max_nt = kFastThreads) {
+  const int cap = env_max_threads();
+  return make_geometry(batch, channels, voxels, num_bins, soft, include_background != 0, labels,
+                       env_steps("ACE_FWD_STEPS"), env_copies(), moments,
+                       fast_forward(soft, labels, act, channels, moments), max_nt < cap ? max_nt : cap);
+}
+
+// The activation is not an argument here: the largest workspace of the
+// layouts a call may use (generic, fast, soft moments).
+size_t workspace_size(int64_t batch, int64_t channels, int64_t voxels, int num_bins, int binning,
+                      int include_background, int target_kind) {
   const bool soft = binning == ACE_SOFT;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
-  return make_geometry(batch, channels, voxels, num_bins, soft, include_background != 0, labels,
-                       env_steps("ACE_FWD_STEPS"), env_copies(),
-                       soft && labels && fast_channels(channels));
+  size_t best = 0;
+  for (int act : {(int)kActNone, (int)kActSoftmax}) {
+    for (int max_nt : {kThreads, kFastThreads}) {
+      const bool moments = use_moments(soft, labels, act, batch, channels, voxels, num_bins,
+                                       include_background);
+      const Geometry g = forward_geometry(batch, channels, voxels, num_bins, soft,
+                                          include_background, labels, act, moments, max_nt);
+      best = g.ws_bytes > best ? g.ws_bytes : best;
+    }
+  }
+  return best;
+}
+
+// fast_bin's fixed point and edge margin for K bins (ace_bins.hpp:
+// fast_bin_consts).
+void set_fast_bins(FwdParams& p, int num_bins, int64_t channels) {
+  const FastBinConsts f = fast_bin_consts(num_bins, channels);
+  p.qscale = f.qscale;
+  p.qlo = f.qlo;
+  p.qhi = f.qhi;
+  p.qmq = f.qmq;
+  p.qmask = f.qmask;
+  p.qs = f.qs;
+  p.pscale = f.pscale;
 }
 
 // Kernel parameters of one forward problem (geometry g, workspace at ws).
@@ -172,6 +220,9 @@ FwdParams fwd_params(const void* x, int x_dtype, const void* target, bool labels
   p.ignore_empty = ignore_empty_classes != 0;
   p.red = reduction;
   p.empty_w = empty_weight;
+  p.packed = g.packed ? 1 : 0;
+  p.pscale = 1.0 / 1073741824.0;  // the generic kernels' sums: 30-bit fixed point
+  if (g.fast && !moments) set_fast_bins(p, num_bins, channels);
   if (moments) {
     const MomentScale ms = moment_scale(num_bins);
     p.msc = ldexpf(1.0f, ms.m);
@@ -239,12 +290,9 @@ BwdParams bwd_params(const void* x, int x_dtype, const void* target, bool labels
 // Bytes of one level's workspace region in a multi-level call.
 size_t level_ws_bytes(int64_t batch, int64_t channels, int64_t voxels, int num_bins, int binning,
                       int include_background) {
-  const Geometry g = workspace_geometry(batch, channels, voxels, num_bins, binning,
-                                        include_background, ACE_TARGET_LABELS_I64);
-  const Geometry h = make_geometry(batch, channels, voxels, num_bins, binning == ACE_SOFT,
-                                   include_background != 0, true, env_steps("ACE_FWD_STEPS"),
-                                   env_copies());
-  return align_up(g.ws_bytes > h.ws_bytes ? g.ws_bytes : h.ws_bytes, 256);
+  return align_up(workspace_size(batch, channels, voxels, num_bins, binning, include_background,
+                                 ACE_TARGET_LABELS_I64),
+                  256);
 }
 
 template <typename T>
@@ -291,13 +339,8 @@ size_t ace_workspace_bytes(int64_t batch, int64_t channels, int64_t voxels, int 
                            int binning, int x_dtype, int include_background, int target_kind) {
   (void)x_dtype;
   if (batch < 1 || channels < 1 || voxels < 0 || num_bins < 1) return 0;
-  const Geometry g = workspace_geometry(batch, channels, voxels, num_bins, binning,
-                                        include_background, target_kind);
-  const Geometry h = make_geometry(batch, channels, voxels, num_bins, binning == ACE_SOFT,
-                                   include_background != 0,
-                                   target_kind == ACE_TARGET_LABELS_I64,
-                                   env_steps("ACE_FWD_STEPS"), env_copies());
-  return g.ws_bytes > h.ws_bytes ? g.ws_bytes : h.ws_bytes;
+  return workspace_size(batch, channels, voxels, num_bins, binning, include_background,
+                        target_kind);
 }
 
 size_t ace_workspace_reset_bytes(int64_t batch, int64_t channels, int64_t voxels,
@@ -326,9 +369,8 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
   const bool moments =
       use_moments(soft, labels, act, batch, channels, voxels, num_bins, include_background);
-  const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
-                                   include_background != 0, labels, env_steps("ACE_FWD_STEPS"),
-                                   env_copies(), moments);
+  const Geometry g = forward_geometry(batch, channels, voxels, num_bins, soft, include_background,
+                                      labels, act, moments);
   if (workspace_bytes < g.ws_bytes) return ACE_EWORKSPACE;
   if (g.lds_fwd > kMaxLds) return ACE_EUNSUPPORTED;
   if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
@@ -394,8 +436,20 @@ int ace_forward_levels(int levels, const AceFwdLevel* lv, int x_dtype, int64_t b
     return ACE_EINVAL;
   if (!fast_channels(channels)) return ACE_EUNSUPPORTED;
   const bool soft = binning == ACE_SOFT;
+  // every level in one launch: one block size for all of them -- 1024
+  // threads when each level's geometry allows it, else 256
+  int max_nt = kFastThreads;
+  for (int l = 0; l < levels; ++l) {
+    if (lv[l].voxels < 0) return ACE_EINVAL;
+    const bool moments = use_moments(soft, true, kActSoftmax, batch, channels, lv[l].voxels,
+                                     num_bins, include_background);
+    const Geometry g = forward_geometry(batch, channels, lv[l].voxels, num_bins, soft,
+                                        include_background, true, kActSoftmax, moments, max_nt);
+    if (g.nt != kFastThreads) max_nt = kThreads;
+  }
   FwdLevels L{};
   L.n = levels;
+  L.nt = max_nt;
   long long nblk = 0;
   size_t lds = 0, off = 0;
   int cmax = 0;
@@ -409,9 +463,8 @@ int ace_forward_levels(int levels, const AceFwdLevel* lv, int x_dtype, int64_t b
     const bool moments = use_moments(soft, true, kActSoftmax, batch, channels, v.voxels, num_bins,
                                      include_background);
     if (soft && !moments) return ACE_EUNSUPPORTED;
-    const Geometry g = make_geometry(batch, channels, v.voxels, num_bins, soft,
-                                     include_background != 0, true, env_steps("ACE_FWD_STEPS"),
-                                     env_copies(), moments);
+    const Geometry g = forward_geometry(batch, channels, v.voxels, num_bins, soft,
+                                        include_background, true, kActSoftmax, moments, max_nt);
     if (g.lds_fwd > kMaxLds) return ACE_EUNSUPPORTED;
     if (nblk + g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
     L.lv[l] = fwd_params(v.x, x_dtype, v.target, true, v.voxels, batch, channels, num_bins,

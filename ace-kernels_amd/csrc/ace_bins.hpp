@@ -3,12 +3,15 @@
 // a binary search at every float32 near every boundary).
 #pragma once
 
+#include <stdint.h>
+
+#include <cmath>
+
 #if defined(__HIPCC__)
 #include <hip/hip_runtime.h>
 #define ACE_HD __host__ __device__ __forceinline__
 #else
 #include <algorithm>
-#include <cmath>
 #define ACE_HD inline
 #endif
 
@@ -81,6 +84,61 @@ template <bool RIGHT>
 ACE_HD int bucket_unit(float p, float nf, const float* tab) {
   const int g = bucket_guess(p, nf);
   return bucket_fix<RIGHT>(g, tab[g + 1], p);
+}
+
+// Fast bins (the hard forward kernels with class labels: ace_core.hpp,
+// fast_exp / fast_bin): with n = K bins a probability is held as
+// q = trunc(p n 2^qs), n 2^qs <= 2^30.  Its bin is k = z >> qs, z = q
+// clamped to [2^(qs-1), (2n - 1) 2^(qs-1)] (t = p n clamped to [1/2, n - 1/2],
+// away from the outer edges 0 and n), and it is "near" an interior edge
+// when z lies within qmq of a multiple of 2^qs.  The margin qmq is n 2^-18
+// of t (C <= 4 channels) or n 2^-17 (more), in units of 2^-qs: twice the
+// fast probabilities' relative error bound (3e-6 at C = 16) plus the edges'
+// offsets from (j + 1) / n (8 2^-24 relative, see bucket_unit).  Beyond 512
+// bins the margin is half a bin: every value is near, and the kernels take
+// the exact path throughout.
+struct FastBinConsts {
+  float qscale;      // n 2^qs
+  uint32_t qlo, qhi; // 2^(qs-1), (2n - 1) 2^(qs-1)
+  uint32_t qmq;      // margin
+  uint32_t qmask;    // 2^qs - 1
+  int qs;
+  double pscale;     // 1 / (n 2^qs): the value of one unit of q
+};
+
+inline FastBinConsts fast_bin_consts(int n, long long channels) {
+  int c = 0;
+  while ((1ll << c) < n) ++c;  // ceil(log2 n)
+  const int qs = 30 - c;
+  FastBinConsts f;
+  f.qs = qs;
+  f.qscale = (float)std::ldexp((double)n, qs);
+  f.qlo = 1u << (qs - 1);
+  f.qhi = (uint32_t)(2 * n - 1) << (qs - 1);
+  f.qmask = (1u << qs) - 1;
+  unsigned long long mq = ((unsigned long long)n << qs) >> (channels <= 4 ? 18 : 17);
+  if (mq < 1) mq = 1;
+  if (n > 512) mq = 1ull << (qs - 1);
+  f.qmq = (uint32_t)mq;
+  f.pscale = 1.0 / std::ldexp((double)n, qs);
+  return f;
+}
+
+// The bin of q and whether q is near an interior edge (see FastBinConsts).
+ACE_HD uint32_t med3_u32(uint32_t a, uint32_t lo, uint32_t hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint32_t r;
+  asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(lo), "v"(hi));
+  return r;
+#else
+  return a < lo ? lo : (a > hi ? hi : a);
+#endif
+}
+ACE_HD bool fast_bin_index(uint32_t q, uint32_t qlo, uint32_t qhi, uint32_t qmq, uint32_t qmask,
+                           int qs, uint32_t& k) {
+  const uint32_t z = med3_u32(q, qlo, qhi);
+  k = z >> qs;
+  return ((z + qmq) & qmask) < 2 * qmq;
 }
 
 // Fixed point of the soft moments (per half-bin sums of p and p^2).  A

@@ -60,6 +60,17 @@ struct FwdParams {
   int lchunk;          // log2 of the copies one lane adds before unpacking
   int epi_all;         // one block runs every batch index's epilogue and the loss
   float empty_w;
+  int packed;          // hard binning with labels: final sums W << 32 | G, then P
+  // fast hard kernels (softmax + class labels, fast_bin): with n = K bins, a
+  // probability p is held as q = trunc(p n 2^qs), its bin as q >> qs (q
+  // clamped to [qlo, qhi]), and it is "near" an edge when the clamped q lies
+  // within qmq of a multiple of 2^qs (ace_bins.hpp: FastBinConsts)
+  float qscale;        // n 2^qs
+  uint32_t qlo, qhi;   // 2^(qs-1) and (2n - 1) 2^(qs-1): t = p n clamped to [1/2, n - 1/2]
+  uint32_t qmq;        // the edge margin in units of 2^-qs of t
+  uint32_t qmask;      // 2^qs - 1
+  int qs;
+  double pscale;       // value of one unit of the hard sums of p (fast: 1 / (K 2^qs), else 2^-30)
   float msc;           // soft moments: 2^m, the fixed-point scale of p (moment_scale)
   float misc;          // 2^-m
   int mw;              // soft moments: half-bin h has base h mw (in units of 2^-m)
@@ -387,37 +398,38 @@ __device__ __forceinline__ void load_tables(float* lds, const float* btab, const
   for (int i = threadIdx.x; i < nrepl; i += kThreads) lds[n + 2 + i] = rtab[i];
 }
 
-// A thread's share of the LDS tables -- entries tid and tid + kThreads of the
-// padded bucket table and of the centre table -- held in registers, so that a
-// kernel can issue these loads, then its first tiles' loads, and only then
-// wait for the tables (in-order vmcnt, a partial wait) and write them to LDS.
-// The loads are unconditional (clamped in-bounds indices, unused values
+// A thread's share of the LDS tables -- entries tid and tid + nt (the block
+// size) of the padded bucket table and of the centre table -- held in registers, so
+// that a kernel can issue these loads, then its first tiles' loads, and only
+// then wait for the tables (in-order vmcnt, a partial wait) and write them to
+// LDS.  The loads are unconditional (clamped in-bounds indices, unused values
 // discarded): a load under a branch would make the compiler wait for every
 // outstanding load instead.
 struct TableRegs {
   float b[2], r[2];  // raw table values; padding applied when stored
-  __device__ __forceinline__ void load(const float* btab, const float* rtab, int n, int nrepl) {
+  // nt: the block size (a compile-time kThreads where the kernel has one)
+  __device__ __forceinline__ void load(const float* btab, const float* rtab, int n, int nrepl,
+                                       int nt) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int i = (int)threadIdx.x + u * kThreads;
+      const int i = (int)threadIdx.x + u * nt;
       b[u] = btab[min(max(i - 1, 0), n - 1)];
       r[u] = nrepl > 0 ? rtab[min(i, nrepl - 1)] : 0.0f;
     }
   }
   // bscale: a power of two the bucket table is multiplied by (exact)
   __device__ __forceinline__ void store(float* lds, const float* btab, const float* rtab, int n,
-                                        int nrepl, float bscale = 1.0f) const {
+                                        int nrepl, int nt, float bscale = 1.0f) const {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int i = (int)threadIdx.x + u * kThreads;
+      const int i = (int)threadIdx.x + u * nt;
       if (i < n + 2) lds[i] = i == 0 ? -__builtin_inff() : (i <= n ? b[u] * bscale : __builtin_inff());
       if (i < nrepl) lds[n + 2 + i] = r[u];
     }
-    // tables longer than 2 x kThreads entries
-    for (int i = (int)threadIdx.x + 2 * kThreads; i < n + 2; i += kThreads)
+    // tables longer than 2 x nt entries
+    for (int i = (int)threadIdx.x + 2 * nt; i < n + 2; i += nt)
       lds[i] = i == n + 1 ? __builtin_inff() : btab[i - 1] * bscale;
-    for (int i = (int)threadIdx.x + 2 * kThreads; i < nrepl; i += kThreads)
-      lds[n + 2 + i] = rtab[i];
+    for (int i = (int)threadIdx.x + 2 * nt; i < nrepl; i += nt) lds[n + 2 + i] = rtab[i];
   }
 };
 
@@ -653,7 +665,7 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
                                           const float* repl, int CK, int CL, int b0, int nb) {
   const int tid = threadIdx.x;
   const int K = P.K;
-  const int NV = fin_values(CK, MOM);
+  const int NV = fin_values(CK, MOM, P.packed != 0);
   const int reps = P.reps;
   const EpiLayout L = epi_layout(CK, CL, nb, MOM);
   const int NB = nb * CK;  // bins of this epilogue
@@ -664,8 +676,8 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
   float* sf = reinterpret_cast<float*>(hist + L.sf);        // [nb * CL]
   double* terms = reinterpret_cast<double*>(hist + L.terms);  // [nb * 2CK][6]
   const int64_t BCK = (int64_t)P.B * CK;
-  const double dscale = 1.0 / 1073741824.0;
-  const double mscale = (double)P.misc;
+  const double dscale = 1.0 / 1073741824.0;  // W and G of the unpacked sums
+  const double pscale = P.pscale;             // the sums of p (hard)
   if constexpr (MOM) {
     // per half-bin: the five moments (every replica in flight at once), then
     // its six contributions
@@ -678,6 +690,7 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
       load_sums<5>(fb, NV, reps, H2, th, m);  // every replica's loads in flight at once
       zero_sums<5>(fb, NV, reps, H2, th);
       const int hh = th % (2 * K);
+      const double mscale = (double)P.misc;
       const double L = (double)((long long)hh * P.mw) * mscale;
       moment_terms((double)m[0], (double)m[1], (double)m[2] * mscale,
                    (double)m[3] * (mscale * mscale * (double)(1ll << P.mshift)),
@@ -712,10 +725,17 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
           Gd += tb[6 * hh + 5];
         }
       }
+    } else if (P.packed) {
+      // W << 32 | G (unsigned: W may reach 2^31), then the sum of p
+      zero_sums<2>(fb_of(i), NV, reps, CK, t);
+      const unsigned long long wg = (unsigned long long)sm[0];
+      Wd = (double)(wg >> 32);
+      Gd = (double)(wg & 0xffffffffull);
+      Pd = (double)sm[1] * pscale;
     } else {
       zero_sums<3>(fb_of(i), NV, reps, CK, t);
       Wd = (double)sm[0] * dscale;
-      Pd = (double)sm[1] * dscale;
+      Pd = (double)sm[1] * pscale;
       Gd = (double)sm[2] * dscale;
     }
     const int64_t o = (int64_t)(b0 + bb) * CK + t;
@@ -741,9 +761,17 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
   } else {
     for (int i0 = tid; i0 < NB; i0 += 2 * kThreads) {
       const int i1 = i0 + kThreads < NB ? i0 + kThreads : i0;
-      long long s0[3], s1[3];
-      load_sums<3>(fb_of(i0), NV, reps, CK, i0 - (nb == 1 ? 0 : i0 / CK) * CK, s0);
-      load_sums<3>(fb_of(i1), NV, reps, CK, i1 - (nb == 1 ? 0 : i1 / CK) * CK, s1);
+      long long s0[3] = {0, 0, 0}, s1[3] = {0, 0, 0};
+      if (P.packed) {
+        long long a0[2], a1[2];
+        load_sums<2>(fb_of(i0), NV, reps, CK, i0 - (nb == 1 ? 0 : i0 / CK) * CK, a0);
+        load_sums<2>(fb_of(i1), NV, reps, CK, i1 - (nb == 1 ? 0 : i1 / CK) * CK, a1);
+        s0[0] = a0[0]; s0[1] = a0[1];
+        s1[0] = a1[0]; s1[1] = a1[1];
+      } else {
+        load_sums<3>(fb_of(i0), NV, reps, CK, i0 - (nb == 1 ? 0 : i0 / CK) * CK, s0);
+        load_sums<3>(fb_of(i1), NV, reps, CK, i1 - (nb == 1 ? 0 : i1 / CK) * CK, s1);
+      }
       bin(i0, s0);
       if (i1 != i0) bin(i1, s1);
     }
@@ -951,8 +979,16 @@ __device__ __forceinline__ void block_sums_r(const FwdParams& P, const Hist& H, 
     if constexpr (!SOFT) {
       long long n = 0, g = 0;
       sum_packed<R>(H.a, t * R, t, chunk, n, g, s1);
+      if (labels) {
+        // fin layout [2][CK] (P.packed): the counts share one word, W << 32 | G
+        // (a batch index has fewer than 2^32 voxels per channel row)
+        const unsigned long long wg = ((unsigned long long)n << 32) | (unsigned long long)g;
+        if (wg) atomicAdd(&fin[t], wg);
+        if (s1) atomicAdd(&fin[CK + t], (unsigned long long)s1);
+        continue;
+      }
       s0 = n << kFrac;
-      s2 = labels ? (g << kFrac) : sum_copies<R>(H.g1, t * R, t);
+      s2 = sum_copies<R>(H.g1, t * R, t);
     } else {
       s0 = sum_copies<R>(H.w, t * R, t);
       s1 = sum_copies<R>(H.p, t * R, t);
@@ -996,15 +1032,17 @@ __device__ __forceinline__ void block_sums(const FwdParams& P, const Hist& H, in
 // (tile % reps) of batch b's final sums (fixed point: exact and
 // order-independent).  Ticket counters, each on its own 256-byte line, then
 // pick the last block of each group of gs tiles, the last group of batch b
-// (which runs b's epilogue) and the last batch epilogue to start (which sums
-// the per-class errors into the loss in a fixed order).
+// (which runs b's epilogue; with one group per batch index the group's last
+// block, one round trip sooner) and the last batch epilogue to start (which
+// sums the per-class errors into the loss in a fixed order).  Runs in the
+// block's first kThreads threads.
 template <bool SOFT, bool MOM>
 __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, unsigned char* hist,
                                            const float* repl, int CK, int CL, int b,
                                            int64_t tile, bool labels) {
   const int tid = threadIdx.x;
   unsigned long long* fin =
-      P.fin + ((int64_t)b * P.reps + tile % P.reps) * fin_values(CK, MOM);
+      P.fin + ((int64_t)b * P.reps + tile % P.reps) * fin_values(CK, MOM, P.packed != 0);
   if constexpr (MOM)
     block_moments(P, H, CK, fin);
   else
@@ -1019,12 +1057,17 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
     int* gc = counter(P, (int64_t)b * P.gpb + g);
     if (ticket(gc) == (int)gsize - 1) {
       __hip_atomic_store(gc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // the last group of batch b -- or, with one epilogue block for all
-      // batch indices, the last group of all
-      int* bc = counter(P, (int64_t)P.B * P.gpb + (P.epi_all ? 0 : b));
-      const int arrivals = P.epi_all ? (int)(P.B * P.gpb) : (int)P.gpb;
-      last = ticket(bc) == arrivals - 1;
-      if (last) __hip_atomic_store(bc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (P.gpb == 1) {
+        // one group per batch index (and epi_all implies one batch index)
+        last = 1;
+      } else {
+        // the last group of batch b -- or, with one epilogue block for all
+        // batch indices, the last group of all
+        int* bc = counter(P, (int64_t)P.B * P.gpb + (P.epi_all ? 0 : b));
+        const int arrivals = P.epi_all ? (int)(P.B * P.gpb) : (int)P.gpb;
+        last = ticket(bc) == arrivals - 1;
+        if (last) __hip_atomic_store(bc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     s_last = last;
   }
@@ -1416,6 +1459,52 @@ __device__ __forceinline__ void softmax_fast(float (&x)[C]) {
   for (int c = 0; c < C; ++c) x[c] = div_rn(x[c], s, y);
 }
 
+// Fast bins (softmax over C channels), for the hard forward kernels with
+// class labels.  With n = K bins, each loss channel's probability is held as
+// q = trunc(p~ n 2^qs), where
+// p~ = e_c / s with e_c = exp2((x_c - max) log2 e) and s = e_0 + ... + e_{C-1}
+// from the hardware's v_exp_f32 and v_rcp_f32 (three VALU instructions per
+// channel for the exponential instead of the nine of exp_neg, no correctly
+// rounded division).  The bin is k = z >> qs with z = q clamped to
+// [2^(qs-1), (2n - 1) 2^(qs-1)] (t = p n clamped to [1/2, n - 1/2]).
+//
+// p~ is not the correctly rounded softmax: its relative error is below
+// 3e-6 for C <= 16 and p >= 1 / (2n) (a, the exponent, rounded twice and
+// times the float log2 e: 1.3e-7 |a|; v_exp_f32 and v_rcp_f32 1 ulp each; the
+// sum's C - 1 roundings and the other terms' exponent errors), and measured
+// on MI355X below 5.4e-7 over 2^24 random logit vectors at C = 4.  The bin
+// edges lie within (j + 1) 8 2^-24 of the integers j + 1 in units of t
+// (torch's float32 linspace, see bucket_unit).  So whenever z is at least the
+// margin qmq (n 2^-18 of t for C <= 4, n 2^-17 above: twice the error bound
+// plus the edge offsets) away from every multiple of 2^qs, k is the bin of
+// the exact probability, on either side of `right`.  Otherwise -- or when
+// the sum is NaN (NaN or infinite logits) -- the channel is "near" and takes
+// the exact path (softmax_fast, bucket_unit), the path the backward kernels
+// always take.  The largest logit's term is exactly 1 (x - max = 0), so a
+// saturated voxel gets p~ = 1 exactly, as the exact path does.
+template <int C>
+__device__ __forceinline__ void fast_exp(const float (&x)[C], const FwdParams& P, float (&e)[C],
+                                         float& rq, bool& nan) {
+  constexpr float kLog2e = 0x1.715476p+0f;
+  const float m = max_of<C>(x);
+  e[0] = __builtin_amdgcn_exp2f((x[0] - m) * kLog2e);
+  float s = e[0];
+#pragma unroll
+  for (int c = 1; c < C; ++c) {
+    e[c] = __builtin_amdgcn_exp2f((x[c] - m) * kLog2e);
+    s += e[c];
+  }
+  rq = __builtin_amdgcn_rcpf(s) * P.qscale;
+  nan = !(s == s);
+}
+// q, the bin k and whether the channel is near an edge, from e_c and n 2^qs / s
+// (ace_bins.hpp: fast_bin_index).
+__device__ __forceinline__ bool fast_bin(float e, float rq, const FwdParams& P, uint32_t& q,
+                                         uint32_t& k) {
+  q = cvt_u32(e * rq);
+  return fast_bin_index(q, P.qlo, P.qhi, P.qmq, P.qmask, P.qs, k);
+}
+
 // softmax_fast with every probability scaled by sc = 2^m (the fixed-point
 // scale of the histograms, isc = 2^-m): q = e y sc, r = e - (s isc) q,
 // p = q + r y sc are the steps of div_rn with both factors scaled by powers
@@ -1455,30 +1544,45 @@ __device__ __forceinline__ uint32_t packed_high(uint32_t X, int c) {
   return __builtin_amdgcn_perm(X, 1u << (kShiftN - 32), 0x0c02040cu + ((uint32_t)c << 8));
 }
 
-// One tile into the histogram copies.  hb[c]: this lane's copy of channel c's
-// bin 0 (u64 words), bins R words = 1 << lsh bytes apart.  skip0: channel 0
-// (background) is not in the loss.
-template <int C, int VEC, bool SOFT, bool RIGHT, bool skip0>
-__device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const float* tab,
-                                                const MomentScaleArgs& ms, int K, int lsh,
+// One (voxel, channel) into the hard histogram copies.  hb: this lane's
+// copy of the channel's bin 0 (u64 words), bins R words = 1 << lsh bytes
+// apart; k the bin, q = trunc(p K 2^qs), hi the high word of the packed
+// increment (count | label count).
+__device__ __forceinline__ void accumulate_hard(uint32_t k, uint32_t q, uint32_t hi, int lsh,
+                                                unsigned long long* hb) {
+  lds_add(bin_at(hb, (int)k, lsh), ((unsigned long long)hi << 32) | q);
+}
+
+// High word of a voxel's packed increment for channel c: 1 << 21 (count)
+// | (label == c) << 10 (label count).  X = label_bytes(label) (C <= 4), lc =
+// fast_label(label).
+template <int C>
+__device__ __forceinline__ uint32_t high_word(uint32_t X, uint32_t lc, int c) {
+  if constexpr (C <= 4)
+    return packed_high(X, c);
+  else
+    return lc == (uint32_t)c ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32))) : (1u << (kShiftN - 32));
+}
+
+// Soft binning, one tile: the correctly rounded softmax computed directly
+// scaled by 2^m (softmax_fixed, the moments' fixed-point scale; the bucket
+// table in LDS is scaled the same way), the half-bin h by one table read and
+// one comparison, and the moments of the offset u = trunc(p 2^m) - h w
+// (moment_scale) -- exact for the quantised p, which the soft gradient needs
+// in bins of a few voxels (d enters it amplified by 1 / S = 2K).  C <= 4: two
+// voxels at a time, every table read issued before the atomics (the reads
+// cannot pass an LDS atomic); C = 16: one voxel at a time.
+template <int C, int VEC, bool RIGHT, bool SKIP0>
+__device__ __forceinline__ void soft_accumulate(const FastTile<C, VEC>& t, const float* tab,
+                                                const FwdParams& P, int K, int lsh,
                                                 unsigned long long* const (&hb)[C],
                                                 const size_t words) {
-  // probabilities come scaled by 2^30 (hard) or 2^m (soft moments) from
-  // softmax_fixed, the bucket table too
-  const float sc = SOFT ? ms.sc : 0x1p30f;
-  const float isc = SOFT ? ms.isc : 0x1p-30f;
-  const float nf = (float)(SOFT ? 2 * K : K) * isc;
-  // C <= 4: all VEC voxels at a time -- every bin guess first, then every
-  // table read, then the corrections and atomics.  The table reads cannot
-  // move past an LDS atomic (same LDS array), so this order keeps VEC * C
-  // reads in flight instead of waiting for each one; the blocks are all
-  // resident at 4 waves per SIMD, so up to 128 registers per lane cost
-  // nothing.  C = 16: one voxel at a time, each table read just before its
-  // use (the batched form would need more than 128 registers).
+  const float sc = P.msc;
+  const float isc = P.misc;
+  const int nw = -P.mw;
+  const float nf = (float)(2 * K) * isc;
   constexpr bool BATCH = C <= 4;
-  // soft: two voxels at a time (four would hold 111 VGPRs at C = 4, leaving
-  // exactly the 4 waves per SIMD the 1024 blocks need)
-  constexpr int NJ = BATCH ? (SOFT && VEC > 2 ? 2 : VEC) : 1;
+  constexpr int NJ = BATCH ? (VEC > 2 ? 2 : VEC) : 1;
 #pragma unroll
   for (int j0 = 0; j0 < VEC; j0 += NJ) {
     float p[NJ][C];
@@ -1499,55 +1603,104 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
       for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
         for (int c = 0; c < C; ++c)
-          if (!(c == 0 && skip0)) e[jj][c] = tab[g[jj][c] + 1];
+          if (!(c == 0 && SKIP0)) e[jj][c] = tab[g[jj][c] + 1];
     }
 #pragma unroll
     for (int jj = 0; jj < NJ; ++jj) {
-      if constexpr (!SOFT) {
+      // moments of the voxel's half-bin h: count | labelled count | sum u
+      // packed as in hard binning, sum u^2, labelled sum u; u < 2^24 (one
+      // 24-bit multiply-add, u^2 two 24-bit multiplies)
+      unsigned long long* ga = hb[0];
+      uint32_t gq = 0u;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (c == 0 && SKIP0) continue;
+        const int h = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
+        const uint32_t u = mad_i24(h, nw, cvt_u32(p[jj][c]));
+        const bool hit = lab[jj] == (uint32_t)c;
+        const uint32_t hi = hit ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
+                                : (1u << (kShiftN - 32));
+        unsigned long long* a = bin_at(hb[c], h, lsh);
+        lds_add(a, ((unsigned long long)hi << 32) | u);
+        lds_add(a + words, square_u24(u));
+        ga = hit ? a : ga;
+        gq = hit ? u : gq;
+      }
+      // unconditional: without a labelled loss channel gq is 0 and ga the
+      // first half-bin of channel 0's copy, so the add changes nothing
+      lds_add(ga + 2 * words, (unsigned long long)gq);
+    }
+  }
+}
+
+// One tile into the histogram copies.  Hard binning: every (voxel, loss
+// channel) through fast_bin; the few near an edge are added afterwards
+// through the exact path (correctly rounded softmax, table lookup), so every
+// bin is the exact bin of the reference's float32 probability semantics, and
+// the sums of p carry p~ (the loss and the gradient's sign(d) are within
+// their tolerances of the exact sums).  Soft binning: soft_accumulate.
+// SKIP0: channel 0 (background) is not in the loss.
+template <int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
+__device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const float* tab,
+                                                const FwdParams& P, int K, int lsh,
+                                                unsigned long long* const (&hb)[C],
+                                                const size_t words) {
+  static_assert(C * VEC <= 32, "near flags of a tile in one 32-bit word");
+  if constexpr (SOFT) {
+    soft_accumulate<C, VEC, RIGHT, SKIP0>(t, tab, P, K, lsh, hb, words);
+    return;
+  }
+  uint32_t nearbits = 0;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    float x[C], e[C], rq;
+    bool nan;
+#pragma unroll
+    for (int c = 0; c < C; ++c) x[c] = t.x[c][j];
+    fast_exp<C>(x, P, e, rq, nan);
+    const uint32_t X = C <= 4 ? label_bytes(t.lab[j], C) : 0u;
+    const uint32_t lc = fast_label<C>(t.lab[j]);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (c == 0 && SKIP0) continue;
+      uint32_t q, k;
+      const bool near = fast_bin(e[c], rq, P, q, k) || nan;
+      // k is a valid bin either way (fast_bin clamps it): a near channel adds
+      // 0 here, which keeps the atomics out of a branch, and its value below
+      const uint32_t hi = near ? 0u : high_word<C>(X, lc, c);
+      accumulate_hard(k, near ? 0u : q, hi, lsh, hb[c]);
+      nearbits |= (near ? 1u : 0u) << (j * C + c);
+    }
+  }
+  if (nearbits) {
+    const float nf = (float)K;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const uint32_t bits = (nearbits >> (j * C)) & ((1u << C) - 1u);
+      if (bits) {
+        float p[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) p[c] = t.x[c][j];
+        softmax_fast<C>(p);
+        const uint32_t X = C <= 4 ? label_bytes(t.lab[j], C) : 0u;
+        const uint32_t lc = fast_label<C>(t.lab[j]);
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-          if (c == 0 && skip0) continue;
-          const int k = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
-          const uint32_t q = cvt_u32(p[jj][c]);
-          uint32_t hi;
-          if constexpr (C <= 4)
-            hi = packed_high(label_bytes(t.lab[j0 + jj], C), c);
-          else
-            hi = (lab[jj] == (uint32_t)c) ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
-                                          : (1u << (kShiftN - 32));
-          lds_add(bin_at(hb[c], k, lsh), ((unsigned long long)hi << 32) | q);
+          if ((c == 0 && SKIP0) || !(bits & (1u << c))) continue;
+          const uint32_t k = (uint32_t)bucket_unit<RIGHT>(p[c], nf, tab);
+          const uint32_t q = cvt_u32(p[c] * P.qscale);
+          accumulate_hard(k, q, high_word<C>(X, lc, c), lsh, hb[c]);
         }
-      } else {
-        // soft: moments of the voxel's half-bin h (count | labelled count |
-        // sum u packed as in hard binning, sum u^2, labelled sum u) of the
-        // offset u = trunc(p 2^m) - h w < 2^24 from the half-bin's base
-        // (moment_scale): one 24-bit multiply-add, u^2 two 24-bit multiplies
-        unsigned long long* ga = hb[0];
-        uint32_t gq = 0u;
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-          if (c == 0 && skip0) continue;
-          const int h = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
-          const uint32_t u = mad_i24(h, ms.nw, cvt_u32(p[jj][c]));
-          const bool hit = lab[jj] == (uint32_t)c;
-          const uint32_t hi = hit ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
-                                  : (1u << (kShiftN - 32));
-          unsigned long long* a = bin_at(hb[c], h, lsh);
-          lds_add(a, ((unsigned long long)hi << 32) | u);
-          lds_add(a + words, square_u24(u));
-          ga = hit ? a : ga;
-          gq = hit ? u : gq;
-        }
-        // unconditional: without a labelled loss channel gq is 0 and ga the
-        // first half-bin of channel 0's copy, so the add changes nothing
-        lds_add(ga + 2 * words, (unsigned long long)gq);
       }
     }
   }
 }
 
 // SKIP0: channel 0 (background) is not in the loss (P.off == 1).  blk is the
-// block's index in P's own grid, smem the block's dynamic LDS.
+// block's index in P's own grid, smem the block's dynamic LDS.  Any block
+// size that is a multiple of 256 up to 1024 (kFastThreads, the launch
+// bound): every thread bins its share of the tile, then the first 256
+// threads add the block's sums and run the cross-block protocol.
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
 __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t blk,
                                               unsigned char* smem) {
@@ -1585,13 +1738,14 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
     xr[c] = reinterpret_cast<const T*>(P.x) + ((int64_t)b * C + c) * N + t0;
   const long long* lr_ = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
   const int nfull = P.vec_ok ? nvox / VEC * VEC : 0;
-  const int stride = kThreads * VEC;
+  const int nt = SOFT ? kThreads : (int)blockDim.x;  // soft: 256-thread blocks (fast_bound)
+  const int stride = nt * VEC;
   const int nsteps = nfull / stride;  // steps in which every thread has a full vector
 
   // table loads, then the first tile's loads; the tables are written to LDS
   // and the histogram cleared while the tile is in flight
   TableRegs treg;
-  treg.load(P.btab, P.rtab, n, nrepl);
+  treg.load(P.btab, P.rtab, n, nrepl, nt);
   FastTile<C, VEC> ta, tb;
   const uint32_t v0 = (uint32_t)(tid * VEC);
   // voxel offset of this lane in step j, clamped to the last step: a load
@@ -1611,11 +1765,12 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
     fast_load<T, C, VEC>(ta, px, pl, pipe ? at(0) : 0u, true);
     fast_load<T, C, VEC>(tb, px, pl, pipe ? at(1) : 0u, true);
   }
-  const MomentScaleArgs ms{P.msc, P.misc, -P.mw};
-  treg.store(tabs, P.btab, P.rtab, n, nrepl, SOFT ? ms.sc : 0x1p30f);
+  // soft: the bucket table scaled by 2^m like softmax_fixed's probabilities;
+  // hard: as given (the exact path's bucket_unit)
+  treg.store(tabs, P.btab, P.rtab, n, nrepl, nt, SOFT ? P.msc : 1.0f);
   {
     unsigned long long* h64 = reinterpret_cast<unsigned long long*>(hist);
-    for (size_t i = tid; i < hist_words; i += kThreads) h64[i] = 0ull;
+    for (size_t i = tid; i < hist_words; i += nt) h64[i] = 0ull;
   }
   __syncthreads();
   const float* tab = tabs;
@@ -1631,26 +1786,29 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
   if (nsteps > 0) {
     int i = 0;
     for (; i + 2 < nsteps; i += 2) {
-      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, ms, K, lsh, hb, words);
+      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, P, K, lsh, hb, words);
       fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), true);
-      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, ms, K, lsh, hb, words);
+      fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, P, K, lsh, hb, words);
       fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), true);
     }
-    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, ms, K, lsh, hb, words);
-    if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, ms, K, lsh, hb, words);
+    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, P, K, lsh, hb, words);
+    if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, P, K, lsh, hb, words);
   }
   // remaining full vectors (not every thread has one), then single voxels
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
     fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, true);
-    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, ms, K, lsh, hb, words);
+    fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, P, K, lsh, hb, words);
   }
-  for (int v = nfull + tid; v < nvox; v += kThreads) {
+  for (int v = nfull + tid; v < nvox; v += nt) {
     FastTile<C, 1> t;
     fast_load<T, C, 1>(t, xr, lr_, (uint32_t)v, true);
-    fast_accumulate<C, 1, SOFT, RIGHT, SKIP0>(t, tab, ms, K, lsh, hb, words);
+    fast_accumulate<C, 1, SOFT, RIGHT, SKIP0>(t, tab, P, K, lsh, hb, words);
   }
   __syncthreads();
+  // the block's sums and the cross-block protocol take kThreads threads; the
+  // other waves end here (a barrier waits only for waves that have not ended)
+  if (tid >= kThreads) return;
   fwd_finish<SOFT, SOFT>(P, H, hist, repl, CK, CL, b, tile, true);
 }
 
@@ -1756,7 +1914,7 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
   // tables and this thread's first coefficients, then the first tile's loads;
   // LDS is filled while the tile is in flight
   TableRegs treg;
-  treg.load(P.btab, P.rtab, n, nrepl);
+  treg.load(P.btab, P.rtab, n, nrepl, kThreads);
   const float* cb = P.coef + (int64_t)b * CK;
   const float* db = P.d + (int64_t)b * CK;
   // unconditional loads (clamped indices) so that the waits below stay partial
@@ -1779,7 +1937,7 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
     fast_load<T, C, VEC>(ta, px, pl, pipe ? at(0) : 0u, SOFT);
     fast_load<T, C, VEC>(tb, px, pl, pipe ? at(1) : 0u, SOFT);
   }
-  treg.store(tabs, P.btab, P.rtab, n, nrepl);
+  treg.store(tabs, P.btab, P.rtab, n, nrepl, kThreads);
   if (tid < CK) {
     scoef[tid] = c0;
     if (SOFT) sdd[tid] = d0;
@@ -1839,8 +1997,15 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
 }
 
 // One problem per launch: block blockIdx.x of P's grid.
+// Block size bound: kFastThreads for hard binning with C <= 4; kThreads
+// otherwise (16 channels of two tiles in flight need more than the 128 VGPRs
+// of 16 waves per CU; soft moments run in 256-thread blocks, make_geometry).
+template <int C, bool SOFT>
+constexpr int fast_bound() {
+  return (C <= 4 && !SOFT) ? kFastThreads : kThreads;
+}
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
-__global__ void __launch_bounds__(kThreads) fwd_kernel_fast(const FwdParams P) {
+__global__ void __launch_bounds__((fast_bound<C, SOFT>())) fwd_kernel_fast(const FwdParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   fwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(P, blockIdx.x, smem);
 }
@@ -1859,6 +2024,7 @@ struct FwdLevels {
   FwdParams lv[kMaxLevels];
   long long start[kMaxLevels];  // first block of each level, increasing
   int n;
+  int nt;                       // threads per block, the same for every level
 };
 struct BwdLevels {
   BwdParams lv[kMaxLevels];
@@ -1873,7 +2039,7 @@ __device__ __forceinline__ int level_of(const long long (&start)[kMaxLevels], in
   return l;
 }
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
-__global__ void __launch_bounds__(kThreads) fwd_kernel_fast_levels(const FwdLevels L) {
+__global__ void __launch_bounds__((fast_bound<C, SOFT>())) fwd_kernel_fast_levels(const FwdLevels L) {
   extern __shared__ __align__(16) unsigned char smem[];
   const long long g = blockIdx.x;
   const int l = level_of(L.start, L.n, g);
@@ -1920,26 +2086,32 @@ inline LaunchEvents& launch_events() {
   return ev;
 }
 
-// One launch of `kern` (one by-value parameter block) on kThreads-thread blocks.
+// One launch of `kern` (one by-value parameter block) on nt-thread blocks.
 template <typename Kern, typename Params>
-hipError_t launch(Kern kern, long long nblk, size_t lds, hipStream_t s, const Params& prm) {
+hipError_t launch(Kern kern, long long nblk, size_t lds, hipStream_t s, const Params& prm,
+                  int nt = kThreads) {
   const LaunchEvents& ev = launch_events();
   if (ev.start || ev.stop) {
     void* args[] = {const_cast<Params*>(&prm)};
     return hipExtLaunchKernel(reinterpret_cast<const void*>(kern), dim3((unsigned)nblk),
-                              dim3(kThreads), args, lds, s, ev.start, ev.stop, 0);
+                              dim3((unsigned)nt), args, lds, s, ev.start, ev.stop, 0);
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(kThreads), lds, s, prm);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3((unsigned)nt), lds, s, prm);
   return hipGetLastError();
 }
 
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) {
   auto kern = fwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
+  int nt = kThreads;
   if constexpr (has_fast<CMAX, EXACT>()) {
-    if (prm.act == kActSoftmax && prm.tk == kTgtLabels && (!SOFT || g.moments))
+    // g.fast: softmax with class labels, soft binning in the moments layout
+    // (the host's decision, ace_abi.hip: fast_forward)
+    if (g.fast) {
       kern = prm.off ? fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true>
                      : fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false>;
+      nt = g.nt;
+    }
   }
   if (g.lds_fwd > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1947,7 +2119,7 @@ hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) 
                                        (int)g.lds_fwd);
     if (e != hipSuccess) return e;
   }
-  return launch(kern, g.nblk, g.lds_fwd, s, prm);
+  return launch(kern, g.nblk, g.lds_fwd, s, prm, nt);
 }
 
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
@@ -1980,7 +2152,7 @@ hipError_t launch_fwd_levels_t(long long nblk, size_t lds, const FwdLevels& L, h
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  return launch(kern, nblk, lds, s, L);
+  return launch(kern, nblk, lds, s, L, L.nt);
 }
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, hipStream_t s) {

@@ -7,15 +7,20 @@
 
 namespace ace {
 
-constexpr int kThreads = 256;           // threads per block (4 wave64)
+constexpr int kThreads = 256;           // threads per block (4 wave64); the epilogue's width
+constexpr int kFastThreads = 1024;      // threads per block of the fast forward kernels (16 wave64)
 constexpr int kFrac = 30;               // fixed-point fraction bits of the sums
 constexpr int kMaxChannels = 64;        // largest C with a built kernel
 constexpr size_t kMaxHistLds = 32 * 1024;  // default LDS budget of the histogram copies
 constexpr int kMaxCopyCount = 2047;        // hard: voxels one copy may count (11-bit field)
 constexpr int kCtrStride = 64;             // ints between ticket counters (one 256-byte line each)
 constexpr int kGroupTiles = 16;            // blocks per ticket group
+constexpr int kSingleTicketTiles = 256;    // up to this many blocks per batch index: one ticket level
 constexpr int kRepTiles = 256;             // blocks per replica of the final sums
+constexpr int kRepTilesFast = 64;          // the same for the fast forward's 1024-thread blocks
 constexpr int kMaxReps = 4;                // replicas of the final sums per batch index
+constexpr size_t kMaxFastHistLds = 150 * 1024;  // LDS budget of the histogram copies, 1024-thread blocks
+constexpr int kFastCopies = 16;            // histogram copies of a 1024-thread block
 
 // Channel variants with a compiled kernel: the kernel keeps C logits of VEC
 // voxels in registers.  EXACT variants fix C at compile time; the others
@@ -53,10 +58,13 @@ constexpr size_t hist_bytes_per_copy(int ck, bool soft, bool labels, bool moment
   return moments ? (size_t)ck * 48 : (soft ? (size_t)ck * 24 : (size_t)ck * (labels ? 8 : 16));
 }
 
-// Final sums per batch index and replica: 3 x C'K (W, P, G per bin), or for
-// soft moments 5 x 2C'K (count, label count, sum u, sum u^2 >> shift, sum u
-// over the labelled voxels per half-bin).
-constexpr int fin_values(int ck, bool moments) { return moments ? 10 * ck : 3 * ck; }
+// Final sums per batch index and replica: 3 x C'K (W, P, G per bin); 2 x C'K
+// for hard binning with class labels (W << 32 | G packed in one word, then
+// P); for soft moments 5 x 2C'K (count, label count, sum u, sum u^2 >>
+// shift, sum u over the labelled voxels per half-bin).
+constexpr int fin_values(int ck, bool moments, bool packed = false) {
+  return moments ? 10 * ck : (packed ? 2 * ck : 3 * ck);
+}
 
 // LDS layout of an epilogue over nb batch indices (byte offsets from the
 // histogram region): d, W, G (float) and an empty flag per bin, the per-class
@@ -78,6 +86,9 @@ inline bool fast_channels(int64_t C) { return C == 2 || C == 3 || C == 4 || C ==
 
 struct Geometry {
   Variant var;
+  int nt;              // threads per forward block (kThreads, or kFastThreads for the fast kernels)
+  bool fast;           // the forward runs a fast (softmax + class labels) kernel
+  bool packed;         // hard binning with labels: W and G share one final-sum word
   int C, CL, off, K, ck;
   int64_t B, N;
   int steps;           // vector steps per block
@@ -99,14 +110,17 @@ struct Geometry {
   size_t ws_bytes;     // workspace bytes; all of it starts zero and is left zero
 };
 
-// Blocks per batch index: aim for ~8 blocks per CU on a 256-CU part while
-// keeping every block's tile a whole number of vector steps.
+// Blocks per batch index: aim for ~4 blocks of 256 threads per CU on a
+// 256-CU part (the generic kernels), or one block of 1024 threads per CU (the
+// fast forward kernels: softmax with class labels, `fast`), keeping every
+// block's tile a whole number of vector steps.
 // moments: the soft fast path (softmax + labels, fast_channels(C)) that bins
 // per-half-bin moments instead of per-voxel weights.
 inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
                               bool soft, bool include_background, bool labels,
                               int steps_override = 0, int copies_override = 0,
-                              bool moments = false) {
+                              bool moments = false, bool fast = false,
+                              int max_nt = kFastThreads) {
   Geometry g{};
   g.moments = moments;
   g.var = variant_for(C);
@@ -117,31 +131,56 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   g.ck = g.CL * K;
   g.B = B;
   g.N = N;
-  // histogram copies (lane % copies), within the LDS budget: at most 8 for
-  // hard binning and soft moments -- more copies cut LDS address conflicts
-  // but lengthen the block sums, and on MI355X 8 measured fastest for hard
-  // (cfg 2: 8 ~ 16 < 32 copies); soft moments fill the LDS budget at 8 --
-  // and up to 32 for the generic soft sums
+  g.packed = !soft && labels;
   const size_t per_copy = hist_bytes_per_copy(g.ck, soft, labels, moments);
-  int copies = copies_override > 0 ? copies_override : ((soft && !moments) ? 32 : 8);
-  while (copies > 1 && per_copy * copies > (copies_override > 0 ? 160 * 1024 : kMaxHistLds))
-    copies /= 2;
+  const bool counted = !soft || moments;  // copies count voxels in 11-bit fields
+  // fast forward: 1024-thread blocks (one per CU) with up to kFastCopies
+  // copies, as many as the LDS holds; each copy counts at most kMaxCopyCount
+  // voxels (nt / copies lanes x steps x vec).  When even one vector step per
+  // lane would overflow a copy, the fast kernel runs with 256-thread blocks.
+  int fast_copies = 0, fast_steps_max = 0;
+  if (fast) {
+    int c = copies_override > 0 ? copies_override : kFastCopies;
+    while (c > 1 && per_copy * c > kMaxFastHistLds) c /= 2;
+    fast_copies = c;
+    fast_steps_max = (int)((int64_t)kMaxCopyCount / ((int64_t)(kFastThreads / c) * g.var.vec));
+  }
+  g.fast = fast;
+  // 1024 threads for hard binning with C <= 4 only: the 16-channel kernel's
+  // registers allow 256, and soft moments measured slower in 1024-thread
+  // blocks, whose 48 C'K-byte copies leave fewer copies per lane (MI355X,
+  // cfg 3: 34.9 vs 34.5 us; cfg 5, 50 bins: 70.8 vs 51.2 us)
+  g.nt = (fast && !soft && C <= 4 && fast_steps_max >= 1 && max_nt >= kFastThreads) ? kFastThreads
+                                                                                      : kThreads;
+  int copies;
+  if (g.nt == kFastThreads) {
+    copies = fast_copies;
+  } else {
+    // histogram copies (lane % copies), within the LDS budget: at most 8 for
+    // hard binning and soft moments -- more copies cut LDS address conflicts
+    // but lengthen the block sums, and on MI355X 8 measured fastest for hard
+    // (cfg 2: 8 ~ 16 < 32 copies); soft moments fill the LDS budget at 8 --
+    // and up to 32 for the generic soft sums
+    copies = copies_override > 0 ? copies_override : ((soft && !moments) ? 32 : 8);
+    while (copies > 1 && per_copy * copies > (copies_override > 0 ? 160 * 1024 : kMaxHistLds))
+      copies /= 2;
+  }
   g.copies = copies;
-  const int64_t step_vox = (int64_t)kThreads * g.var.vec;
+  const int64_t step_vox = (int64_t)g.nt * g.var.vec;
   int steps = steps_override;
   if (steps <= 0) {
     const int64_t total = B * (N > 0 ? N : 1);
-    // ~4 blocks per CU; half that above 8 channels, whose kernels hold ~120
-    // VGPRs (4 waves per SIMD: 1024 blocks would just fill the chip, and
-    // on MI355X ~10% of them started a round late) and issue C x K x 3
-    // final-sum atomics per block (cfg 4, C = 16: 52 us at 512 blocks vs
-    // 57 us at 1024)
-    const int64_t target_blocks = C > 8 ? 512 : 1024;
+    // generic kernels: ~4 blocks per CU; half that above 8 channels, whose
+    // kernels hold ~120 VGPRs (4 waves per SIMD: 1024 blocks would just fill
+    // the chip, and on MI355X ~10% of them started a round late) and issue
+    // C x K x 3 final-sum atomics per block (cfg 4, C = 16: 52 us at 512
+    // blocks vs 57 us at 1024).  Fast kernels: one 1024-thread block per CU.
+    const int64_t target_blocks = g.nt == kFastThreads ? 256 : (C > 8 ? 512 : 1024);
     steps = (int)cdiv(total, step_vox * target_blocks);
     if (steps < 1) steps = 1;
     if (steps > 64) steps = 64;
   }
-  if (!soft || moments) {
+  if (counted) {
     // every copy counts at most kMaxCopyCount voxels of a tile
     const int64_t max_steps = (int64_t)kMaxCopyCount * copies / step_vox;
     if (steps > max_steps) steps = (int)(max_steps > 0 ? max_steps : 1);
@@ -149,8 +188,8 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   g.steps = steps;
   // block sums: a lane adds the packed words of as many copies as keep the
   // count fields within kMaxCopyCount before decoding them (a copy counts at
-  // most kThreads / copies lanes x steps x vec voxels)
-  const int64_t copy_vox = (int64_t)(kThreads / copies) * steps * g.var.vec;
+  // most nt / copies lanes x steps x vec voxels)
+  const int64_t copy_vox = (int64_t)(g.nt / copies) * steps * g.var.vec;
   int chunk = copies;
   while (chunk > 1 && (!soft || moments) && chunk * copy_vox > kMaxCopyCount) chunk /= 2;
   int lchunk = 0;
@@ -159,11 +198,13 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   g.tile_vox = step_vox * steps;
   g.tiles = N > 0 ? cdiv(N, g.tile_vox) : 1;
   g.nblk = B * g.tiles;
-  // tickets: groups of kGroupTiles blocks, then the groups of a batch index;
-  // final sums replicated so that ~kRepTiles blocks share a replica
-  g.gs = g.tiles < kGroupTiles ? g.tiles : kGroupTiles;
+  // tickets: one counter per batch index when it has at most
+  // kSingleTicketTiles blocks (one device-scope round trip fewer at the end),
+  // else groups of kGroupTiles blocks, then the groups of a batch index; final
+  // sums replicated so that ~kRepTiles blocks share a replica
+  g.gs = g.tiles <= kSingleTicketTiles ? g.tiles : kGroupTiles;
   g.gpb = cdiv(g.tiles, g.gs);
-  int64_t reps = cdiv(g.tiles, kRepTiles);
+  int64_t reps = cdiv(g.tiles, g.nt == kFastThreads ? kRepTilesFast : kRepTiles);
   g.reps = (int)(reps > kMaxReps ? kMaxReps : reps);
   const int n = soft ? 2 * K : K;
   g.tab_floats = align_up((size_t)(n + 2) + (soft ? (size_t)(2 * K + 2) : 0), 4);
@@ -186,7 +227,7 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   const int64_t counters = B * g.gpb + B + 1;
   g.off_part = align_up((size_t)counters * kCtrStride * sizeof(int), 256);
   g.off_fin = align_up(g.off_part + (size_t)B * sizeof(unsigned long long), 256);
-  const size_t fin_bytes = (size_t)B * g.reps * fin_values(g.ck, moments) * sizeof(unsigned long long);
+  const size_t fin_bytes = (size_t)B * g.reps * fin_values(g.ck, moments, g.packed) * sizeof(unsigned long long);
   g.ws_bytes = align_up(g.off_fin + fin_bytes, 256);
   return g;
 }

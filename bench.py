@@ -5,25 +5,29 @@
 One step = one forward + backward of the loss (``autograd.grad(loss.sum(),
 x)`` through the registry's ``hip_mi355x`` impl) on one batch of synthetic
 inputs already resident in HBM: configuration 2 (hard, B=2, C=4, 128^3
-fp32, int64 labels) for ``value``, configuration 3 (soft, same tensors)
-reported beside it.  Before every launch -- warm-up included -- a 1 GiB
-buffer is read (summed), so that the inputs are not in the 256 MB last-level
-cache and the cache holds no dirty lines (reference method:
-``src/ace_bench/timing.py:48-77``, with a flush larger than MI355X's cache and
-reads instead of writes).  Each step is timed with HIP events on the stream the
-kernels run on; the median of eager execution is ``value`` (the reference's
-method, ``src/ace_bench/timing.py:48-77``); a HIP-graph replay of the same step
-is reported beside it, and forward and backward kernels are also timed alone.
+fp32, int64 labels) for ``value``; configurations 3 (soft, same tensors), 4
+(hard, C=16) and 5 (soft, K=50, bf16, B=32, 512^2) reported beside it under
+``workloads``, each with its forward and backward kernel rooflines.  Before
+every launch -- warm-up included -- a 1 GiB buffer is read (summed), so that
+the inputs are not in the 256 MB last-level cache and the cache holds no
+dirty lines (reference method: ``src/ace_bench/timing.py:48-77``, with a
+flush larger than MI355X's cache and reads instead of writes).  Each step is
+timed with HIP events on the stream the kernels run on; the median of eager
+execution is ``value`` (the reference's method,
+``src/ace_bench/timing.py:48-77``); a HIP-graph replay of the same step is
+reported beside it, and forward and backward kernels are also timed alone.
 
 ``roofline`` is for the dominant kernel: achieved = its algorithmic bytes per
 launch / its mean duration over the timed launches (cold cache; HIP events
 that the kernel's dispatch stamps as it starts and ends, through
 ``ace_set_launch_events``, so they agree with rocprofv3's kernel durations;
 events recorded on the stream around the same launches, which add the
-dispatch gap after the flush, are reported beside them).  ``traffic`` is read from the committed rocprofv3
-FETCH_SIZE / WRITE_SIZE summary when there is one.  ``cpu_baseline`` times the
-reference algorithm (restated in ``oracle/``) fwd+bwd on configuration 2 on
-the host CPU.
+dispatch gap after the flush, are reported beside them).  ``traffic`` is read
+from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+(``profiles/traffic_cfg2.json``) when it was measured on the current kernel
+sources, else null.  ``cpu_baseline`` times the reference algorithm (restated
+in ``oracle/``) fwd+bwd on the host CPU: configuration 2 (``value``), and
+configuration 1 hard and soft and configuration 3 as ``rows``.
 
 Prints ONE JSON line (rank 0).  ``--gpus`` above 1 exits with a message: this
 build runs on one GPU.
@@ -229,6 +233,12 @@ def bench_workload(wl, steps: int, warmup: int, flush):
     name = max(kernels, key=lambda k: kernels[k][0])
     ms, nbytes, per_vox = kernels[name]
     out["dominant"] = {"kernel": name, "ms": ms, "bytes": nbytes, "bytes_per_voxel": per_vox}
+    out["kernel_roofline"] = {
+        k: {"bound": "hbm", "ms_mean": v[0], "bytes_per_launch": v[1], "bytes_per_voxel": v[2],
+            "achieved_GBps": v[1] / (v[0] * 1e-3) / 1e9,
+            "frac": v[1] / (v[0] * 1e-3) / 1e9 / PEAK_HBM_GBPS}
+        for k, v in kernels.items()
+    }
     del graph
     return out
 
@@ -344,15 +354,24 @@ def hard_bin_parity(wl):
             "within_one_ulp_of_an_edge": int((down != up).sum().item()), "moved": moved}
 
 
-def cpu_baseline(budget_s: float = 15.0):
-    """The reference algorithm (oracle restatement, torch CPU) fwd+bwd on the
-    benchmark workload (configuration 2), a bounded number of calls."""
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_time(wl, budget_s: float):
+    """p50 ms of the reference algorithm (oracle restatement, torch CPU)
+    fwd+bwd on workload ``wl``: warm-up, then calls until ``budget_s``
+    (at least 3, at most 50)."""
     import torch
 
-    from ace_kernels.workloads import workload
     from oracle.reference import reference_ace
 
-    wl = workload(2)
     x, y = wl.make("cpu")
 
     def step():
@@ -370,17 +389,39 @@ def cpu_baseline(budget_s: float = 15.0):
         if len(times) >= 50:
             break
     p50 = statistics.median(times)
-    ideal = wl.ideal_bytes("fwd_bwd")
+    return {"workload": wl.name, "binning": wl.config.binning, "ms_p50": p50, "calls": len(times),
+            "effective_GBps": wl.ideal_bytes("fwd_bwd") / (p50 * 1e-3) / 1e9}
+
+
+def cpu_baseline(budget_s: float = 6.0):
+    """The reference algorithm on the host CPU: configuration 2 (the headline,
+    ``value``), configuration 1 hard and soft (the reference's CPU-runnable
+    case) and configuration 3 (soft at the headline shape), each a bounded
+    number of fwd+bwd calls."""
+    import torch
+
+    from ace_kernels.workloads import workload
+
+    import dataclasses
+
+    cfg1 = workload(1)
+    cfg1_soft = dataclasses.replace(cfg1, name=cfg1.name.replace("hard", "soft"),
+                                    config=cfg1.config.model_copy(update={"binning": "soft"}))
+    rows = [cpu_time(workload(2), budget_s), cpu_time(workload(1), budget_s),
+            cpu_time(cfg1_soft, budget_s), cpu_time(workload(3), budget_s)]
+    head = rows[0]
     return {
-        "value": p50,
+        "value": head["ms_p50"],
         "unit": "ms",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{wl.name}: reference loss (B x C bucketize/scatter loop + autograd) "
-                  f"fwd+bwd, {len(times)} calls within {budget_s:.0f} s, p50, "
-                  f"torch CPU intra-op threads",
-        "effective_GBps": ideal / (p50 * 1e-3) / 1e9,
+        "sample": f"{head['workload']}: reference loss (B x C bucketize/scatter loop + autograd) "
+                  f"fwd+bwd, {head['calls']} calls within {budget_s:.0f} s, p50, torch CPU "
+                  f"intra-op threads; rows: the same for cfg 1 hard / soft and cfg 3",
+        "effective_GBps": head["effective_GBps"],
         "host_cpu_count": os.cpu_count(),
+        "cpu_model": cpu_model(),
+        "rows": rows,
     }
 
 
@@ -416,12 +457,27 @@ def profile_kernels(workloads, launches: int) -> None:
     log(f"copy kernel: {launches} x {src.numel() * 4} bytes read + written")
 
 
+def kernel_source_hash() -> str:
+    """SHA-256 (16 hex digits) of the HIP sources the library is built from."""
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = ROOT / "ace-kernels_amd" / "csrc"
+    for f in sorted(csrc.glob("*")) + sorted((ROOT / "include").glob("*.h")):
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def _traffic(kernel: str):
     """HBM bytes per launch of ``kernel`` on configuration 2 from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy
-    kernel), or None when there is no summary."""
+    kernel), or None when there is no summary or it was measured on other
+    kernel sources than these (its recorded source hash differs)."""
     try:
         data = json.loads(TRAFFIC_FILE.read_text())
+        if data.get("source_sha16") != kernel_source_hash():
+            return None
         return data[kernel]["bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
@@ -433,8 +489,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--workloads", default="2,3", help="benchmark workloads (first = value)")
+    ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU baseline row")
+    ap.add_argument("--workloads", default="2,3,4,5", help="benchmark workloads (first = value)")
     ap.add_argument("--no-deepsup", action="store_true", help="skip the deep-supervision steps")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="LAUNCHES",
                     help="only launch the kernels LAUNCHES times each (for rocprofv3)")
@@ -519,7 +575,7 @@ def main() -> int:
         "hard_bin_parity": parity,
     }
     if not args.no_cpu:
-        log("cpu baseline (oracle reference, cfg 2)")
+        log("cpu baseline (oracle reference: cfg 2, cfg 1 hard / soft, cfg 3)")
         line["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(line), flush=True)
     return 0

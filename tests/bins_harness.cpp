@@ -248,6 +248,50 @@ long long check_moment_all(const float* table, int K, int right) {
   return bad;
 }
 
+// The fast bins' margin against their error bound: for every float32 p
+// within `width` ulp of every entry of `table` (the n hard edges), and a
+// sample of [0, 1] every 997 ulp, take the
+// fast path's q at the two ends of the error window, trunc(p n 2^qs
+// (1 -+ rel)); whenever fast_bin_index calls such a q not near an edge, its
+// bin must equal torch.bucketize(p) (left and right).  margin_div > 1
+// plants a margin that many times too small.  Returns the violations.
+long long check_fast_margin(const float* table, int n, int channels, double rel, int width,
+                            int margin_div) {
+  ace::FastBinConsts f = ace::fast_bin_consts(n, channels);
+  if (margin_div > 1) f.qmq = f.qmq / (uint32_t)margin_div;
+  const double scale = std::ldexp((double)n, f.qs);
+  const uint32_t one = to_bits(1.0f);
+  long long bad = 0;
+  auto check = [&](float p) -> long long {
+    long long b = 0;
+    for (int r = 0; r < 2; ++r) {
+      int want = expected(table, n, p, r != 0);
+      if (want > n - 1) want = n - 1;
+      for (double s : {1.0 - rel, 1.0 + rel}) {
+        double qd = std::floor((double)p * scale * s);
+        if (qd < 0) qd = 0;
+        if (qd > scale) qd = scale;
+        uint32_t k;
+        const bool near = ace::fast_bin_index((uint32_t)qd, f.qlo, f.qhi, f.qmq, f.qmask, f.qs, k);
+        if (!near && (int)k != want) ++b;
+      }
+    }
+    return b;
+  };
+#pragma omp parallel for reduction(+ : bad) schedule(dynamic)
+  for (int j = 0; j < n; ++j) {
+    const int64_t e = to_bits(table[j]);
+    for (int64_t d = -width; d <= width; ++d) {
+      const int64_t bits = e + d;
+      if (bits < 0 || bits > (int64_t)one) continue;
+      bad += check(from_bits((uint32_t)bits));
+    }
+  }
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+  for (int64_t bits = 0; bits <= (int64_t)one; bits += 997) bad += check(from_bits((uint32_t)bits));
+  return bad;
+}
+
 // Out-of-domain inputs stay in [0, n - 1] (histogram indices never leave range).
 int check_clamped(const float* table, int n) {
   const std::vector<float> tab = padded(table, n);

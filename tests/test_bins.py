@@ -59,6 +59,9 @@ def harness(tmp_path_factory) -> ctypes.CDLL:
     lib.check_moment_offsets.argtypes = [fp, ctypes.c_int, ctypes.c_int]
     lib.check_moment_all.restype = ctypes.c_longlong
     lib.check_moment_all.argtypes = [fp, ctypes.c_int, ctypes.c_int]
+    lib.check_fast_margin.restype = ctypes.c_longlong
+    lib.check_fast_margin.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_int,
+                                      ctypes.c_int]
     lib.check_unit_nan.restype = ctypes.c_int
     lib.check_unit_nan.argtypes = [fp, ctypes.c_int]
     return lib
@@ -192,3 +195,26 @@ def test_soft_moment_offsets_every_probability(harness, right: bool) -> None:
     """Every float32 in [0, 1] at K = 20: offset in range, and base + offset
     is exactly p 2^m for p >= 2^(23 - m)."""
     assert harness.check_moment_all(_fp(_table(20, True)), 20, int(right)) == 0
+
+
+# the fast probabilities' relative error bound the margin is built on
+# (ace_core.hpp: fast_exp; measured on MI355X: 5.4e-7 at C = 4)
+FAST_REL = {4: 1.5e-6, 16: 3.0e-6}
+
+
+@pytest.mark.parametrize("channels", [4, 16])
+@pytest.mark.parametrize("k", [1, 2, 7, 20, 40, 50, 64, 100, 256, 512])
+def test_fast_bins_margin_covers_the_error_bound(harness, channels: int, k: int) -> None:
+    """A fast-path q anywhere inside the error window of a probability p
+    that fast_bin_index does not flag as near an edge has the bin of p
+    (torch.bucketize, left and right), for every float within 256 ulp of
+    every edge and a sample of [0, 1] (the hard forward's fast path)."""
+    assert harness.check_fast_margin(_fp(_table(k, False)), k, channels, FAST_REL[channels], 256, 1) == 0
+
+
+def test_fast_bins_margin_check_catches_a_small_margin(harness) -> None:
+    """Planted mistake: a margin eight times too small lets fast bins
+    disagree with bucketize near edges."""
+    total = sum(harness.check_fast_margin(_fp(_table(k, False)), k, 4, FAST_REL[4], 256, 8)
+                for k in (20, 50))
+    assert total > 0

@@ -1,6 +1,7 @@
 """Host caches of the HIP impl (tables, class weights, workspace): nothing a
-HIP graph may have captured is ever freed, and nothing is created during a
-capture (CPU tests; the capture state is simulated).  The device-side
+HIP graph may have captured is ever freed, tables and class weights are not
+created during a capture, and a capture's own workspace stays out of eager
+use (CPU tests; the capture state is simulated).  The device-side
 regression test is tests/test_gpu_graph_workspace.py."""
 
 from __future__ import annotations
@@ -50,11 +51,17 @@ def test_nothing_is_created_during_capture(monkeypatch: pytest.MonkeyPatch) -> N
     # cached objects are returned as they are
     assert common.workspace(dev, stream, 4096) is ws
     assert common.bin_tables(23, False, dev) is tab
-    # anything new raises instead of allocating inside the capture
-    with pytest.raises(RuntimeError, match="graph capture"):
-        common.workspace(dev, stream, ws.numel() + 1)
-    with pytest.raises(RuntimeError, match="graph capture"):
-        common.workspace(dev, stream + 7, 16)
+    # a workspace the capture lacks is its own: zeroed, kept for the
+    # process, and not the buffer eager calls on that stream get
+    own = common.workspace(dev, stream, ws.numel() + 1)
+    assert own is not ws and own.numel() > ws.numel() and int(own.sum()) == 0
+    assert any(t is own for t in common._RETIRED)
+    other = common.workspace(dev, stream + 7, 16)
+    monkeypatch.setattr(common, "capturing", lambda device: False)
+    assert common.workspace(dev, stream, 4096) is ws
+    assert common.workspace(dev, stream + 7, 16) is not other
+    monkeypatch.setattr(common, "capturing", lambda device: True)
+    # tables and class weights come from the host: a capture cannot record that
     with pytest.raises(RuntimeError, match="graph capture"):
         common.bin_tables(3001, False, dev)
     with pytest.raises(RuntimeError, match="graph capture"):

@@ -5,9 +5,11 @@ the reference's harness reports them (``src/ace_bench/measure.py:142-212``;
 its own float32 error grows with N, ``docs/report.md:629-633``).
 
 Bars: against the float32 reference, the north-star tolerances (loss rtol
-1e-5, gradient relative L2 1e-4); against the float64 truth, the kernels'
-error must not exceed twice the float32 reference's own (or 1e-6 relative,
-whichever is larger).  With bf16 logits the reference and the truth compute
+1e-5, gradient relative L2 1e-4, and for float32 logits element by element
+rtol 1e-4 / atol 1e-7 with the reference's near-boundary exemption,
+``gpu_helpers.assert_grad_close``, the count of exempted voxels printed);
+against the float64 truth, the kernels' error must not exceed twice the
+float32 reference's own (or 1e-6 relative, whichever is larger).  With bf16 logits the reference and the truth compute
 on the same bf16 values, and since dx is bf16 like the input, their
 gradients are rounded to bf16 before they are compared.  There an element
 whose float32 value lies near a bf16 rounding boundary can round one bf16 ulp
@@ -24,7 +26,7 @@ import torch
 from ace_kernels import ace_loss
 from ace_kernels.measure import rel_err, rel_l2
 from ace_kernels.workloads import workload
-from gpu_helpers import run, say
+from gpu_helpers import assert_grad_close, run, say
 
 pytestmark = pytest.mark.gpu
 
@@ -67,3 +69,7 @@ def test_benchmark_size_against_reference_and_truth(index) -> None:
     assert err["grad_l2_vs_ref"] < grad_bar
     assert err["loss_vs_truth"] <= max(2 * err["ref_loss_vs_truth"], 1e-6)
     assert err["grad_l2_vs_truth"] <= max(2 * err["ref_grad_l2_vs_truth"], 1e-6)
+    if x.dtype == torch.float32:
+        bad = assert_grad_close(grad, grad_ref, x, cfg, truth=grad64)
+        say(f"full size {wl.name}: element-wise rtol 1e-4 / atol 1e-7: "
+            f"{int(bad.sum())} of {bad.numel()} voxels differ, all within 1e-6 of a bin boundary")

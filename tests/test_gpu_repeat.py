@@ -50,5 +50,5 @@ def test_repeated_forwards_are_identical_and_leave_the_workspace_zero(binning, b
     assert torch.equal(losses, want_loss.expand(launches)), losses[losses != want_loss][:8]
     assert int(bad_coef) == 0
     stream = torch.cuda.current_stream().cuda_stream
-    ws = common._WORKSPACES[(torch.cuda.current_device(), stream)][0]
+    ws = common._WORKSPACES[("cuda", torch.cuda.current_device(), stream)]
     assert int(torch.count_nonzero(ws)) == 0
