@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # enums of include/ace_hip.h
 F32, BF16, F16 = 0, 1, 2
@@ -35,7 +35,12 @@ EXPORTS = (
     "ace_workspace_bytes_levels",
     "ace_forward_levels",
     "ace_backward_levels",
+    "ace_forward_noalloc",
 )
+
+# ace_forward_noalloc's scratch (ACE_NOALLOC_SCRATCH_BYTES) and its error code
+NOALLOC_SCRATCH_BYTES = 1 << 20
+ESCRATCH = 4
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -89,6 +94,16 @@ def lib() -> ctypes.CDLL:
         _i, _i, _i, _i,            # include_bg, ignore_empty, reduction, right
         _f, _p, _p, _p,            # empty_weight, class_weight, bin_table, centre_table
         _p, _sz,                   # workspace, bytes
+        _p, _p, _p, _p, _p, _p,    # coef, diff, jac, per_class, loss, stats
+        _p,                        # stream
+    ]
+    handle.ace_forward_noalloc.restype = _i
+    handle.ace_forward_noalloc.argtypes = [
+        _p, _i, _p, _i,            # x, dtype, target, kind
+        _i64, _i64, _i64,          # B, C, N
+        _i, _i, _i,                # K, binning, activation
+        _i, _i, _i, _i,            # include_bg, ignore_empty, reduction, right
+        _f, _p, _p, _p,            # empty_weight, class_weight, bin_table, centre_table
         _p, _p, _p, _p, _p, _p,    # coef, diff, jac, per_class, loss, stats
         _p,                        # stream
     ]

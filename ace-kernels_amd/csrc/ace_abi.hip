@@ -10,6 +10,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "ace_core.hpp"
 #include "ace_hip.h"
 
@@ -317,11 +319,54 @@ hipError_t pick_levels_bwd(bool soft, bool right, int cmax, long long nblk, size
 }  // namespace
 }  // namespace ace
 
+// ---------------------------------------------- allocation-free forward
+// ace_forward_noalloc's workspace: one array per device, zero at load, held
+// until the process ends.  Host code never passes the array's name to a
+// kernel (on the host it is a stand-in, not a device address); it uses the
+// device address that scratch_address() obtains once per device.
+static __device__ __align__(256) unsigned char scratch[ACE_NOALLOC_SCRATCH_BYTES];
+
+namespace ace {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch`, per device
+
+// Device address of the current device's `scratch` (hipGetSymbolAddress on
+// the first call on that device, with that device current).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return to_code(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return ACE_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return to_code(e);
+    if (!ptr) return ACE_EHIP + (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ACE_OK;
+}
+
+// Zero `words` 8-byte words at p (a fill kernel rather than hipMemsetAsync,
+// so that a captured call records no memset node).
+__global__ void __launch_bounds__(kThreads) clear_words(unsigned long long* p, size_t words) {
+  const size_t stride = (size_t)gridDim.x * kThreads;
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < words; i += stride) p[i] = 0ull;
+}
+
+}  // namespace
+}  // namespace ace
+
 using namespace ace;
 
 extern "C" {
 
-int ace_abi_version(void) { return 4; }
+int ace_abi_version(void) { return 5; }
 
 const char* ace_error_string(int code) {
   switch (code) {
@@ -329,6 +374,9 @@ const char* ace_error_string(int code) {
     case ACE_EINVAL: return "invalid argument";
     case ACE_EUNSUPPORTED: return "unsupported configuration (channels > 64 or LDS too large)";
     case ACE_EWORKSPACE: return "workspace smaller than ace_workspace_bytes()";
+    case ACE_ESCRATCH:
+      return "problem needs more workspace than ace_forward_noalloc's scratch "
+             "(ACE_NOALLOC_SCRATCH_BYTES); use ace_forward with a workspace";
     default: break;
   }
   if (code >= ACE_EHIP) return hipGetErrorString((hipError_t)(code - ACE_EHIP));
@@ -534,6 +582,44 @@ int ace_backward_levels(int levels, const AceBwdLevel* lv, int x_dtype, int64_t 
     default: e = pick_levels_bwd<__half>(soft, right != 0, cmax, nblk, lds, L, s); break;
   }
   return to_code(e);
+}
+
+int ace_forward_noalloc(const void* x, int x_dtype, const void* target, int target_kind,
+                        int64_t batch, int64_t channels, int64_t voxels, int num_bins,
+                        int binning, int activation, int include_background,
+                        int ignore_empty_classes, int reduction, int right, float empty_weight,
+                        const float* class_weight, const float* bin_table,
+                        const float* centre_table, float* coef, float* diff, float* jac,
+                        float* per_class, float* loss, double* stats, void* stream) {
+  // the checks ace_forward makes before it looks at the workspace, so that an
+  // invalid call launches nothing
+  int rc = check_common(x, x_dtype, target, target_kind, batch, channels, voxels, num_bins,
+                        binning, activation, bin_table, centre_table, true);
+  if (rc) return rc;
+  if (reduction != ACE_RED_MEAN && reduction != ACE_RED_SUM && reduction != ACE_RED_NONE)
+    return ACE_EINVAL;
+  if (!coef || !diff || !jac || !per_class) return ACE_EINVAL;
+  if (reduction != ACE_RED_NONE && !loss) return ACE_EINVAL;
+  const size_t need = ace_workspace_reset_bytes(batch, channels, voxels, num_bins, binning, x_dtype,
+                                                include_background, target_kind);
+  if (need == 0) return ACE_EINVAL;
+  if (need > ACE_NOALLOC_SCRATCH_BYTES) return ACE_ESCRATCH;
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc) return rc;
+  // the scratch holds whatever the last call on this device left: clear the
+  // bytes that must start zero, in stream order before the forward
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t words = need / sizeof(unsigned long long);
+  const int64_t blocks = cdiv((int64_t)words, (int64_t)kThreads);
+  hipLaunchKernelGGL(clear_words, dim3((unsigned)(blocks < 256 ? blocks : 256)), dim3(kThreads), 0,
+                     s, static_cast<unsigned long long*>(ws), words);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return to_code(e);
+  return ace_forward(x, x_dtype, target, target_kind, batch, channels, voxels, num_bins, binning,
+                     activation, include_background, ignore_empty_classes, reduction, right,
+                     empty_weight, class_weight, bin_table, centre_table, ws,
+                     ACE_NOALLOC_SCRATCH_BYTES, coef, diff, jac, per_class, loss, stats, stream);
 }
 
 int ace_set_launch_events(void* start, void* stop) {

@@ -57,6 +57,7 @@ enum {
   ACE_EINVAL = 1,       /* bad argument (null pointer, size, enum value)     */
   ACE_EUNSUPPORTED = 2, /* valid but not built: e.g. C > 64, LDS too large    */
   ACE_EWORKSPACE = 3,   /* workspace smaller than ace_workspace_bytes()       */
+  ACE_ESCRATCH = 4,     /* ace_forward_noalloc: needs > ACE_NOALLOC_SCRATCH_BYTES */
   ACE_EHIP = 1000       /* + hipError_t of a failed launch                    */
 };
 
@@ -176,6 +177,32 @@ int ace_backward_levels(int levels, const AceBwdLevel* lv, int x_dtype,
                         int binning, int include_background, int right,
                         int grad_output_per_class, const float* bin_table,
                         const float* centre_table, void* stream);
+
+/*
+ * Allocation-free forward.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The same computation and outputs
+ * as ace_forward, whose kernels it launches, with the workspace taken from a
+ * static device array of the library (ACE_NOALLOC_SCRATCH_BYTES, one per
+ * device, held until the process ends) instead of an argument; it calls no
+ * allocating routine.  The array used is the current device's (x and the
+ * outputs must live there).  Before the forward it clears the bytes the
+ * problem needs with a fill kernel on `stream`.  Problems whose
+ * ace_workspace_bytes() exceed ACE_NOALLOC_SCRATCH_BYTES return ACE_ESCRATCH
+ * before any launch.  Every call on a device shares that device's array:
+ * calls that overlap on one device (different streams, or threads without an
+ * order between them) race and must be serialised by the caller.
+ */
+#define ACE_NOALLOC_SCRATCH_BYTES ((size_t)1 << 20)
+int ace_forward_noalloc(const void* x, int x_dtype, const void* target,
+                        int target_kind, int64_t batch, int64_t channels,
+                        int64_t voxels, int num_bins, int binning,
+                        int activation, int include_background,
+                        int ignore_empty_classes, int reduction, int right,
+                        float empty_weight, const float* class_weight,
+                        const float* bin_table, const float* centre_table,
+                        float* coef, float* diff, float* jac, float* per_class,
+                        float* loss, double* stats, void* stream);
 
 /*
  * Kernel timing.  This has no counterpart in the reference, whose benchmark

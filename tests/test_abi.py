@@ -98,3 +98,41 @@ def test_level_entry_points_validate_before_launch() -> None:
                                    None) == 1
     assert lib.ace_backward_levels(2, bwd, _lib.F32, 2, 16, 20, _lib.HARD, 1, 0, 0, None, None,
                                    None) == 1                              # null bin table
+
+
+def _noalloc_args(x, target, batch, voxels, binning, num_bins, table, centre, outputs):
+    return [x, _lib.F32, target, _lib.TARGET_LABELS_I64, batch, 4, voxels, num_bins, binning,
+            _lib.ACT_SOFTMAX, 1, 1, _lib.RED_MEAN, 0, 0.01, None, table, centre, *outputs, None, None]
+
+
+def test_noalloc_validates_and_rejects_oversize_before_launch() -> None:
+    """ace_forward_noalloc returns before any HIP call on invalid arguments
+    and on problems whose workspace exceeds its scratch (the pointers below
+    are never dereferenced on the host, and nothing is launched)."""
+    lib = _lib.lib()
+    assert b"scratch" in lib.ace_error_string(_lib.ESCRATCH)
+    fake = 256  # non-null stand-ins: validation only checks for null
+    outs = [fake] * 5
+    assert lib.ace_forward_noalloc(*_noalloc_args(None, fake, 2, 64, _lib.HARD, 20, fake, None, outs)) == 1
+    assert lib.ace_forward_noalloc(*_noalloc_args(fake, fake, 2, 64, _lib.SOFT, 20, fake, None, outs)) == 1
+    # 200 batch indices of 50-bin soft moments: > 1 MiB of final sums
+    big = lib.ace_workspace_bytes(200, 4, 64, 50, _lib.SOFT, _lib.F32, 1, 0)
+    assert big > _lib.NOALLOC_SCRATCH_BYTES
+    rc = lib.ace_forward_noalloc(*_noalloc_args(fake, fake, 200, 64, _lib.SOFT, 50, fake, fake, outs))
+    assert rc == _lib.ESCRATCH
+    # the benchmark configurations fit
+    for args in [(2, 4, 128 ** 3, 20, _lib.HARD), (2, 4, 128 ** 3, 20, _lib.SOFT),
+                 (1, 16, 128 ** 3, 20, _lib.HARD), (32, 4, 512 ** 2, 50, _lib.SOFT)]:
+        b, c, n, k, binning = args
+        assert lib.ace_workspace_bytes(b, c, n, k, binning, _lib.F32, 1, 0) <= _lib.NOALLOC_SCRATCH_BYTES
+
+
+def test_noalloc_source_calls_no_allocator() -> None:
+    """The allocation-free forward's host code names no allocating routine."""
+    src = (Path(__file__).resolve().parents[1] / "ace-kernels_amd" / "csrc" / "ace_abi.hip").read_text()
+    start = src.index("// ---------------------------------------------- allocation-free forward")
+    end = src.index("int ace_set_launch_events")
+    body = src[start:end]
+    for name in ("hipMalloc", "hipFree", "hipHostMalloc", "hipMallocAsync", "hipExtMalloc", "malloc(", "new "):
+        assert name not in body, name
+    assert "hipGetSymbolAddress" in body and "HIP_SYMBOL(scratch)" in body
