@@ -483,6 +483,94 @@ def _traffic(kernel: str):
         return None
 
 
+COPY_KIB = 262144.0  # profile_kernels' calibration copy: 256 MiB read and 256 MiB written
+
+
+def _profile_key(name: str, workloads):
+    """(kernel, workload index) of a dispatch in a ``--profile-kernels`` run
+    over ``workloads`` (one hard, one soft workload), or ("copy", None)."""
+    if "copyBuffer" in name:
+        return "copy", None
+    if "ace::" not in name or "levels" in name:
+        return None
+    kernel = "ace_fwd" if "fwd_kernel" in name else "ace_bwd" if "bwd_kernel" in name else None
+    if kernel is None:
+        return None
+    args = [a.strip() for a in name[name.index("<") + 1:name.index(">")].split(",")]
+    # fast kernels: <T, C, VEC, SOFT, RIGHT, SKIP0>; generic: <T, CMAX, EXACT, VEC, SOFT, RIGHT>
+    soft = args[3] == "true" if "_fast" in name else args[4] == "true"
+    from ace_kernels.workloads import workload
+
+    for idx in workloads:
+        if (workload(idx).config.binning == "soft") == soft:
+            return kernel, idx
+    return None
+
+
+def summarize_profiles(dirs, workloads) -> int:
+    """Summarise rocprofv3 ``--pmc`` runs of ``bench.py --profile-kernels``
+    (the ``*counter_collection.csv`` files under ``dirs``): the median of each
+    counter per kernel and workload as a markdown table on stdout.  With
+    FETCH_SIZE and WRITE_SIZE present, both are scaled by what they read for
+    the calibration copy (the largest copy dispatches, 256 MiB each way) and
+    the first workload's HBM bytes per launch are written to TRAFFIC_FILE
+    with the hash of the kernel sources they were measured on."""
+    import csv
+
+    values = {}
+    for d in dirs:
+        for f in sorted(Path(d).rglob("*counter_collection.csv")):
+            with open(f, newline="") as fh:
+                for r in csv.DictReader(fh):
+                    key = _profile_key(r["Kernel_Name"], workloads)
+                    if key is not None:
+                        values.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(
+                            float(r["Counter_Value"]))
+    if not values:
+        print("no counter_collection.csv rows of the ace kernels found", file=sys.stderr)
+        return 1
+
+    def copy_median(counter: str):
+        v = values.get(("copy", None), {}).get(counter, [])
+        big = [x for x in v if x >= 0.5 * max(v)] if v else []
+        return statistics.median(big) if big else None
+
+    counters = sorted({c for k in values if k[0] != "copy" for c in values[k]})
+    keys = sorted(k for k in values if k[0] != "copy")
+    print("| counter | " + " | ".join(f"{k} cfg{i}" for k, i in keys) + " |")
+    print("|---|" + "---:|" * len(keys))
+    for c in counters:
+        cells = [f"{statistics.median(values[k][c]):.1f}" if c in values[k] else "" for k in keys]
+        print(f"| {c} | " + " | ".join(cells) + " |")
+    fetch_copy, write_copy = copy_median("FETCH_SIZE"), copy_median("WRITE_SIZE")
+    if fetch_copy and write_copy:
+        from ace_kernels.workloads import workload
+
+        fs, ws = COPY_KIB / fetch_copy, COPY_KIB / write_copy
+        print(f"\ncopy kernel: FETCH_SIZE {fetch_copy:.1f} KiB, WRITE_SIZE {write_copy:.1f} KiB "
+              f"for {COPY_KIB:.0f} KiB each way; scale factors fetch x{fs:.4f}, write x{ws:.4f}\n")
+        print("| kernel | workload | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) | "
+              "algorithmic bytes | ratio |")
+        print("|---|---|---:|---:|---:|---:|---:|")
+        out = {"source_sha16": kernel_source_hash(), "workload": workloads[0]}
+        for kernel, idx in keys:
+            f_kib = statistics.median(values[(kernel, idx)].get("FETCH_SIZE", [float("nan")]))
+            w_kib = statistics.median(values[(kernel, idx)].get("WRITE_SIZE", [float("nan")]))
+            wl = workload(idx)
+            xb, tb = wl.input_bytes(), wl.target_bytes()
+            # as bench_workload: the hard backward reads no labels
+            algo = xb + tb if kernel == "ace_fwd" else 2 * xb + (tb if wl.config.binning == "soft" else 0)
+            hbm = int((f_kib * fs + w_kib * ws) * 1024)
+            print(f"| {kernel} | cfg{idx} | {f_kib:.1f} | {w_kib:.1f} | {hbm} | {algo} | "
+                  f"{hbm / algo:.4f} |")
+            if idx == workloads[0]:
+                out[kernel] = {"bytes_per_launch": hbm, "fetch_kib": f_kib, "write_kib": w_kib,
+                               "fetch_scale": fs, "write_scale": ws, "algorithmic_bytes": algo}
+        TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+        print(f"\nwrote {TRAFFIC_FILE.relative_to(ROOT)} (kernel sources {out['source_sha16']})")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -494,7 +582,12 @@ def main() -> int:
     ap.add_argument("--no-deepsup", action="store_true", help="skip the deep-supervision steps")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="LAUNCHES",
                     help="only launch the kernels LAUNCHES times each (for rocprofv3)")
+    ap.add_argument("--summarize-profiles", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc runs of --profile-kernels (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_profiles:
+        sys.path.insert(0, str(ROOT / "ace-kernels_amd"))
+        return summarize_profiles(args.summarize_profiles, [int(v) for v in args.workloads.split(",")])
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the loss on ONE GPU; --gpus above 1 is not supported "
               "(a multi-GPU run would shard the voxels and all-reduce the 3*B*C'*K integer bin sums "
