@@ -14,11 +14,11 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # enums of include/ace_hip.h
-F32, BF16, F16 = 0, 1, 2
-TARGET_LABELS_I64, TARGET_ONEHOT_F32 = 0, 1
+F32, BF16, F16, F64 = 0, 1, 2, 3
+TARGET_LABELS_I64, TARGET_ONEHOT_F32, TARGET_ONEHOT_F64 = 0, 1, 2
 HARD, SOFT = 0, 1
 ACT_NONE, ACT_SOFTMAX, ACT_SIGMOID = 0, 1, 2
 RED_MEAN, RED_SUM, RED_NONE = 0, 1, 2
@@ -36,6 +36,8 @@ EXPORTS = (
     "ace_forward_levels",
     "ace_backward_levels",
     "ace_forward_noalloc",
+    "ace_forward_f64",
+    "ace_backward_f64",
 )
 
 # ace_forward_noalloc's scratch (ACE_NOALLOC_SCRATCH_BYTES) and its error code
@@ -106,6 +108,28 @@ def lib() -> ctypes.CDLL:
         _f, _p, _p, _p,            # empty_weight, class_weight, bin_table, centre_table
         _p, _p, _p, _p, _p, _p,    # coef, diff, jac, per_class, loss, stats
         _p,                        # stream
+    ]
+    _d = ctypes.c_double
+    handle.ace_forward_f64.restype = _i
+    handle.ace_forward_f64.argtypes = [
+        _p, _p, _i,                # x, target, kind
+        _i64, _i64, _i64,          # B, C, N
+        _i, _i, _i,                # K, binning, activation
+        _i, _i, _i, _i,            # include_bg, ignore_empty, reduction, right
+        _d, _p, _p, _p,            # empty_weight, class_weight, bin_table, centre_table
+        _p, _sz,                   # workspace, bytes
+        _p, _p, _p, _p, _p, _p,    # coef, diff, jac, per_class, loss, stats
+        _p,                        # stream
+    ]
+    handle.ace_backward_f64.restype = _i
+    handle.ace_backward_f64.argtypes = [
+        _p, _p, _i,
+        _i64, _i64, _i64,
+        _i, _i, _i, _i, _i,        # K, binning, activation, include_bg, right
+        _p, _p,                    # bin_table, centre_table
+        _p, _p, _p,                # coef, diff, jac
+        _p, _i,                    # grad_output, per_class
+        _p, _p,                    # dx, stream
     ]
     handle.ace_backward.restype = _i
     handle.ace_backward.argtypes = [

@@ -36,7 +36,7 @@ EPS32 = torch.finfo(torch.float32).eps
 
 _CACHE_LOCK = threading.Lock()
 _TABLES: Dict[Tuple[int, bool, str, int], Tuple[torch.Tensor, Optional[torch.Tensor]]] = {}
-_CLASS_WEIGHTS: Dict[Tuple[Tuple[float, ...], str, int], torch.Tensor] = {}
+_CLASS_WEIGHTS: Dict[Tuple[Tuple[float, ...], str, int, str], torch.Tensor] = {}
 
 
 def _device_key(device: torch.device) -> Tuple[str, int]:
@@ -105,14 +105,16 @@ def class_weights(config: ACEConfig, n_ch: int) -> Optional[List[float]]:
     return weights
 
 
-def class_weight_tensor(weights: Tuple[float, ...], device: torch.device) -> torch.Tensor:
-    """The weights as a float32 device tensor, cached for the life of the process."""
-    key = (tuple(float(w) for w in weights), *_device_key(device))
+def class_weight_tensor(weights: Tuple[float, ...], device: torch.device,
+                        dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """The weights as a float32 (or ``dtype``) device tensor, cached for the
+    life of the process."""
+    key = (tuple(float(w) for w in weights), *_device_key(device), str(dtype))
     with _CACHE_LOCK:
         hit = _CLASS_WEIGHTS.get(key)
         if hit is None:
             _refuse_under_capture(device, "the class-weight tensor")
-            hit = torch.tensor(key[0], dtype=torch.float32, device=device)
+            hit = torch.tensor(key[0], dtype=dtype, device=device)
             _CLASS_WEIGHTS[key] = hit
         return hit
 

@@ -16,9 +16,11 @@ int64 class indices (one-hot conversion fused into the kernels), else as
 raises ``ValueError`` (``common.py:104-105``), a target/input shape mismatch
 ``AssertionError`` (``common.py:117-118``), bad class weights ``ValueError``.
 
-float64 input is rejected with ``TypeError``: every kernel computes in
-float32 (the reference's GPU path falls back to a PyTorch implementation for
-float64, ``v6_triton.py:226-227``; this package has no non-HIP path).
+float64 input runs the float64 kernels (``ace_forward_f64`` /
+``ace_backward_f64``), which compute everything in double with float64
+outputs -- the reference sends float64 to its handwritten "recompute"
+backward in torch (``v6_triton.py:226-227``); this package has no non-HIP
+path.  Their targets are int64 class indices or a float64 one-hot.
 """
 
 from __future__ import annotations
@@ -33,7 +35,8 @@ from ace_kernels.common import bin_tables, class_weight_tensor, class_weights, w
 from ace_kernels.config import ACEConfig
 from ace_kernels.registry import register
 
-_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16,
+           torch.float64: _lib.F64}
 _REDUCTIONS = {"mean": _lib.RED_MEAN, "sum": _lib.RED_SUM, "none": _lib.RED_NONE}
 
 
@@ -61,8 +64,6 @@ def make_plan(input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> P
         raise ValueError(f"input must be [B, C, *spatial], got {tuple(input.shape)}")
     if input.device.type != "cuda":
         raise ValueError(f"hip_mi355x needs a HIP ('cuda') tensor, got {input.device}")
-    if input.dtype == torch.float64:
-        raise TypeError("hip_mi355x computes in float32: float64 input is not supported")
     code = _DTYPES.get(input.dtype)
     x = input if code is not None else input.float()
     code = _DTYPES[x.dtype]
@@ -98,9 +99,10 @@ def make_plan(input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> P
                 f"({tuple(input.shape)})"
             )
         t = target.reshape(b, c, n)
-        if t.dtype != torch.float32:
-            t = t.float()
-        pl.target, pl.target_kind = t.contiguous(), _lib.TARGET_ONEHOT_F32
+        if code == _lib.F64:
+            pl.target, pl.target_kind = t.double().contiguous(), _lib.TARGET_ONEHOT_F64
+        else:
+            pl.target, pl.target_kind = t.float().contiguous(), _lib.TARGET_ONEHOT_F32
     pl.btab, pl.rtab = bin_tables(pl.K, pl.soft, x.device)
     return pl
 
@@ -132,7 +134,8 @@ def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False, shared: bool =
     binning = _lib.SOFT if pl.soft else _lib.HARD
     dims = (pl.B, pl.C, pl.N, pl.K, binning, pl.dtype_code, int(pl.include_bg), pl.target_kind)
     ws = workspace(dev, stream, _workspace_bytes(dims))
-    f32 = torch.float32
+    f64 = pl.dtype_code == _lib.F64
+    f32 = torch.float64 if f64 else torch.float32  # the outputs' type
     # coef, d and jac (all saved for backward) share one allocation; the
     # per-class errors and the loss, which the caller may receive and modify
     # in place, have their own
@@ -151,17 +154,29 @@ def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False, shared: bool =
     loss = torch.empty((), dtype=f32, device=dev) if reduction != _lib.RED_NONE else None
     st = torch.empty((3, pl.B, pl.CL, pl.K), dtype=torch.float64, device=dev) if stats else None
     weights = class_weights(config, pl.CL)
-    cw = class_weight_tensor(tuple(weights), dev) if weights is not None else None
-    rc = lib.ace_forward(
-        pl.x.data_ptr(), pl.dtype_code, pl.target.data_ptr(), pl.target_kind,
-        pl.B, pl.C, pl.N, pl.K, binning, pl.act,
-        int(pl.include_bg), int(config.ignore_empty_classes), reduction, int(pl.right),
-        float(config.empty_weight), _ptr(cw), pl.btab.data_ptr(), _ptr(pl.rtab),
-        ws.data_ptr(), ws.numel(),
-        coef.data_ptr(), d.data_ptr(), jac.data_ptr(), per_class.data_ptr(), _ptr(loss), _ptr(st),
-        stream,
-    )
-    _lib.check(rc, "ace_forward")
+    cw = class_weight_tensor(tuple(weights), dev, f32) if weights is not None else None
+    if f64:
+        rc = lib.ace_forward_f64(
+            pl.x.data_ptr(), pl.target.data_ptr(), pl.target_kind,
+            pl.B, pl.C, pl.N, pl.K, binning, pl.act,
+            int(pl.include_bg), int(config.ignore_empty_classes), reduction, int(pl.right),
+            float(config.empty_weight), _ptr(cw), pl.btab.data_ptr(), _ptr(pl.rtab),
+            ws.data_ptr(), ws.numel(),
+            coef.data_ptr(), d.data_ptr(), jac.data_ptr(), per_class.data_ptr(), _ptr(loss),
+            _ptr(st), stream,
+        )
+        _lib.check(rc, "ace_forward_f64")
+    else:
+        rc = lib.ace_forward(
+            pl.x.data_ptr(), pl.dtype_code, pl.target.data_ptr(), pl.target_kind,
+            pl.B, pl.C, pl.N, pl.K, binning, pl.act,
+            int(pl.include_bg), int(config.ignore_empty_classes), reduction, int(pl.right),
+            float(config.empty_weight), _ptr(cw), pl.btab.data_ptr(), _ptr(pl.rtab),
+            ws.data_ptr(), ws.numel(),
+            coef.data_ptr(), d.data_ptr(), jac.data_ptr(), per_class.data_ptr(), _ptr(loss),
+            _ptr(st), stream,
+        )
+        _lib.check(rc, "ace_forward")
     if loss is None:
         loss = per_class.view(pl.B, pl.CL, *([1] * pl.spatial_ndim))
     return loss, coef, d, jac, per_class, st
@@ -175,12 +190,26 @@ def hip_backward(pl: Plan, coef: torch.Tensor, d: torch.Tensor, jac: torch.Tenso
     stream = _stream(dev)
     per_class = grad_output.dim() > 0
     go = grad_output
-    if go.dtype != torch.float32:
-        go = go.float()
+    f64 = pl.dtype_code == _lib.F64
+    go_dtype = torch.float64 if f64 else torch.float32
+    if go.dtype != go_dtype:
+        go = go.to(go_dtype)
     go = go.reshape(-1) if per_class else go.reshape(())
     if not go.is_contiguous():
         go = go.contiguous()
     dx = torch.empty_like(pl.x)
+    if f64:
+        rc = lib.ace_backward_f64(
+            pl.x.data_ptr(), pl.target.data_ptr() if pl.soft else None, pl.target_kind,
+            pl.B, pl.C, pl.N, pl.K, _lib.SOFT if pl.soft else _lib.HARD, pl.act,
+            int(pl.include_bg), int(pl.right),
+            pl.btab.data_ptr(), _ptr(pl.rtab),
+            coef.data_ptr(), d.data_ptr(), jac.data_ptr(),
+            go.data_ptr(), int(per_class),
+            dx.data_ptr(), stream,
+        )
+        _lib.check(rc, "ace_backward_f64")
+        return dx.view(pl.in_shape)
     rc = lib.ace_backward(
         pl.x.data_ptr(), pl.dtype_code,
         pl.target.data_ptr() if pl.soft else None, pl.target_kind,
@@ -271,10 +300,11 @@ def _(input: torch.Tensor, target: torch.Tensor, config_json: str) -> Outputs:
     config = _config(config_json)
     b, c = input.shape[:2]
     cl = c - (1 if (not config.include_background and c > 1) else 0)
-    per_bin = input.new_empty((b, cl, config.num_bins), dtype=torch.float32)
+    out = torch.float64 if input.dtype == torch.float64 else torch.float32
+    per_bin = input.new_empty((b, cl, config.num_bins), dtype=out)
     loss_shape = (b, cl, *([1] * (input.dim() - 2))) if config.reduction == "none" else ()
-    loss = input.new_empty(loss_shape, dtype=torch.float32)
-    jac = input.new_empty((b, cl), dtype=torch.float32)
+    loss = input.new_empty(loss_shape, dtype=out)
+    jac = input.new_empty((b, cl), dtype=out)
     return loss, per_bin, torch.empty_like(per_bin), jac
 
 

@@ -34,6 +34,9 @@ def _check_plans(plans: Sequence[Plan]) -> None:
     if not 1 <= len(plans) <= MAX_LEVELS:
         raise ValueError(f"ace_loss_levels takes 1 to {MAX_LEVELS} levels, got {len(plans)}")
     p0 = plans[0]
+    if p0.dtype_code == _lib.F64:
+        raise TypeError("ace_loss_levels takes float32 / bfloat16 / float16 logits; "
+                        "call ace_loss per level for float64")
     if p0.act != _lib.ACT_SOFTMAX or p0.target_kind != _lib.TARGET_LABELS_I64:
         raise ValueError("ace_loss_levels needs activation='softmax' with to_onehot_y class labels")
     for p in plans[1:]:

@@ -362,11 +362,19 @@ __global__ void __launch_bounds__(kThreads) clear_words(unsigned long long* p, s
 }  // namespace
 }  // namespace ace
 
+namespace ace {
+namespace f64 {
+// ace_f64.hip: workspace bytes of ace_forward_f64
+size_t workspace_bytes(int64_t batch, int64_t channels, int64_t voxels, int num_bins, int binning,
+                       int include_background);
+}  // namespace f64
+}  // namespace ace
+
 using namespace ace;
 
 extern "C" {
 
-int ace_abi_version(void) { return 5; }
+int ace_abi_version(void) { return 6; }
 
 const char* ace_error_string(int code) {
   switch (code) {
@@ -385,8 +393,9 @@ const char* ace_error_string(int code) {
 
 size_t ace_workspace_bytes(int64_t batch, int64_t channels, int64_t voxels, int num_bins,
                            int binning, int x_dtype, int include_background, int target_kind) {
-  (void)x_dtype;
   if (batch < 1 || channels < 1 || voxels < 0 || num_bins < 1) return 0;
+  if (x_dtype == ACE_F64)
+    return f64::workspace_bytes(batch, channels, voxels, num_bins, binning, include_background);
   return workspace_size(batch, channels, voxels, num_bins, binning, include_background,
                         target_kind);
 }

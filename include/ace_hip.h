@@ -40,10 +40,10 @@
 extern "C" {
 #endif
 
-/* element type of x (and of dx) */
-enum { ACE_F32 = 0, ACE_BF16 = 1, ACE_F16 = 2 };
-/* target layout */
-enum { ACE_TARGET_LABELS_I64 = 0, ACE_TARGET_ONEHOT_F32 = 1 };
+/* element type of x (and of dx); ACE_F64 only through the _f64 entry points */
+enum { ACE_F32 = 0, ACE_BF16 = 1, ACE_F16 = 2, ACE_F64 = 3 };
+/* target layout; ACE_TARGET_ONEHOT_F64 only through the _f64 entry points */
+enum { ACE_TARGET_LABELS_I64 = 0, ACE_TARGET_ONEHOT_F32 = 1, ACE_TARGET_ONEHOT_F64 = 2 };
 /* binning (ACEConfig.binning) */
 enum { ACE_HARD = 0, ACE_SOFT = 1 };
 /* activation applied in-kernel; softmax over C == 1 must be passed as NONE */
@@ -126,6 +126,39 @@ int ace_backward(const void* x, int x_dtype, const void* target,
                  const float* diff, const float* jac,
                  const float* grad_output, int grad_output_per_class,
                  void* dx, void* stream);
+
+/*
+ * Float64 logits: the loss and its gradient computed in double throughout,
+ * outputs in double.  Replaces the reference's float64 route
+ * (src/ace_kernels/impls/v6_triton.py:226-227: float64 input goes to the
+ * handwritten "recompute" backward in torch, impls/v2_autograd.py:196-236,
+ * with float64 softmax / sigmoid, bins and epilogue).  Arguments as
+ * ace_forward / ace_backward, with x, dx, the outputs, `empty_weight`,
+ * `class_weight` and `grad_output` in double; targets are int64 class ids
+ * (ACE_TARGET_LABELS_I64) or a float64 [B, C, N] one-hot
+ * (ACE_TARGET_ONEHOT_F64); the tables are the same float32 tables (converted
+ * exactly).  The workspace is ace_workspace_bytes(..., x_dtype = ACE_F64,
+ * ...), zero at the start and left zero, as for ace_forward.  Results are
+ * deterministic (fixed-order float64 sums, no float atomics).  C <= 64.
+ */
+int ace_forward_f64(const double* x, const void* target, int target_kind,
+                    int64_t batch, int64_t channels, int64_t voxels,
+                    int num_bins, int binning, int activation,
+                    int include_background, int ignore_empty_classes,
+                    int reduction, int right, double empty_weight,
+                    const double* class_weight, const float* bin_table,
+                    const float* centre_table, void* workspace,
+                    size_t workspace_bytes, double* coef, double* diff,
+                    double* jac, double* per_class, double* loss,
+                    double* stats, void* stream);
+int ace_backward_f64(const double* x, const void* target, int target_kind,
+                     int64_t batch, int64_t channels, int64_t voxels,
+                     int num_bins, int binning, int activation,
+                     int include_background, int right,
+                     const float* bin_table, const float* centre_table,
+                     const double* coef, const double* diff,
+                     const double* jac, const double* grad_output,
+                     int grad_output_per_class, double* dx, void* stream);
 
 /*
  * Several levels of one loss in one launch per direction (deep supervision:

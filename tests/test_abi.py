@@ -19,7 +19,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "ace_hip.h"
 def _declared() -> list:
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ace_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ace_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_header_declares_the_binding_exports() -> None:
@@ -136,3 +136,29 @@ def test_noalloc_source_calls_no_allocator() -> None:
     for name in ("hipMalloc", "hipFree", "hipHostMalloc", "hipMallocAsync", "hipExtMalloc", "malloc(", "new "):
         assert name not in body, name
     assert "hipGetSymbolAddress" in body and "HIP_SYMBOL(scratch)" in body
+
+
+def test_f64_entry_points_validate_before_launch() -> None:
+    """ace_forward_f64 / ace_backward_f64 reject bad arguments before any HIP
+    call; ace_workspace_bytes sizes their workspace for x_dtype ACE_F64."""
+    lib = _lib.lib()
+    fake = 256
+    fwd = [None, fake, _lib.TARGET_LABELS_I64, 2, 4, 64, 20, _lib.HARD, _lib.ACT_SOFTMAX,
+           1, 1, _lib.RED_MEAN, 0, 0.01, None, fake, None, fake, 1 << 20, fake, fake, fake, fake,
+           fake, None, None]
+    assert lib.ace_forward_f64(*fwd) == 1  # null x
+    fwd[0] = fake
+    fwd[2] = _lib.TARGET_ONEHOT_F32  # float64 path takes labels or a float64 one-hot
+    assert lib.ace_forward_f64(*fwd) == 1
+    fwd[2] = _lib.TARGET_LABELS_I64
+    fwd[4] = 65
+    assert lib.ace_forward_f64(*fwd) == 2  # C > 64
+    fwd[4] = 4
+    fwd[18] = 16  # workspace too small
+    assert lib.ace_forward_f64(*fwd) == 3
+    bwd = [None, None, _lib.TARGET_LABELS_I64, 2, 4, 64, 20, _lib.HARD, _lib.ACT_SOFTMAX, 1, 0,
+           fake, None, fake, None, fake, fake, 0, fake, None]
+    assert lib.ace_backward_f64(*bwd) == 1  # null x
+    ws = lib.ace_workspace_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F64, 1, 0)
+    assert ws > lib.ace_workspace_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F32, 1, 0) > 0
+    assert ws % 256 == 0

@@ -148,3 +148,27 @@ def test_binding_runs_golden_cases_on_the_device(monkeypatch, name: str) -> None
     (grad,) = torch.autograd.grad(loss.sum(), x)
     torch.testing.assert_close(loss.detach().cpu(), case.loss, rtol=1e-5, atol=1e-7)
     torch.testing.assert_close(grad.cpu(), case.grad, rtol=1e-4, atol=1e-7)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["paper-3d-hard", "paper-3d-soft"])
+def test_binding_runs_float64_on_the_device(monkeypatch, name: str) -> None:
+    """The binding's float64 route (ace_forward_f64 / ace_backward_f64)
+    against the oracle's float64 restatement of the reference's route."""
+    from golden_cases import load_golden
+    from oracle.v2 import v2_ace
+
+    ns = load_binding(monkeypatch)
+    fn = ns["__registered__"]["hip_mi355x"]
+    case = load_golden()[name]
+    cfg = ACEConfig(**case.config)
+    x64 = case.input.double()
+    x = x64.cuda().requires_grad_(True)
+    loss = fn(x, case.target.cuda(), cfg)
+    assert loss.dtype == torch.float64
+    (grad,) = torch.autograd.grad(loss.sum(), x)
+    leaf = x64.clone().requires_grad_(True)
+    want = v2_ace(leaf, case.target, cfg)
+    (want_grad,) = torch.autograd.grad(want.sum(), leaf)
+    torch.testing.assert_close(loss.detach().cpu(), want.detach(), rtol=1e-10, atol=1e-13)
+    torch.testing.assert_close(grad.cpu(), want_grad, rtol=1e-9, atol=1e-13)
