@@ -178,6 +178,23 @@ size_t workspace_size(int64_t batch, int64_t channels, int64_t voxels, int num_b
   return best;
 }
 
+// Vector steps per backward block: ACE_BWD_STEPS, else make_geometry's
+// choice (~1024 blocks; 512 above 8 channels, where the forward's final-sum
+// atomics set the count) -- except the fast 16-channel backward with every
+// channel in the loss, which holds 4 waves per SIMD (ace_core.hpp:
+// bwd_min_waves) and measured fastest with ~1024 blocks on MI355X (cfg 4:
+// 50.8 vs 57.2 us at 512).
+int bwd_steps(bool soft, bool labels, int act, int64_t batch, int64_t channels, int64_t voxels,
+              int include_background, bool moments) {
+  const int env = env_steps("ACE_BWD_STEPS");
+  if (env > 0) return env;
+  const bool fast = act == kActSoftmax && fast_channels(channels) && (!soft || (labels && moments));
+  if (!(fast && channels > 8 && (include_background != 0 || channels == 1))) return 0;
+  const int64_t step_vox = (int64_t)kThreads * variant_for(channels).vec;
+  const int64_t steps = cdiv(batch * (voxels > 0 ? voxels : 1), step_vox * 1024);
+  return (int)(steps < 1 ? 1 : (steps > 64 ? 64 : steps));
+}
+
 // fast_bin's fixed point and edge margin for K bins (ace_bins.hpp:
 // fast_bin_consts).
 void set_fast_bins(FwdParams& p, int num_bins, int64_t channels) {
@@ -455,9 +472,10 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
   const bool moments =
       use_moments(soft, labels, act, batch, channels, voxels, num_bins, include_background);
-  const Geometry g = make_geometry(batch, channels, voxels, num_bins, soft,
-                                   include_background != 0, labels, env_steps("ACE_BWD_STEPS"), 0,
-                                   moments);
+  const Geometry g = make_geometry(
+      batch, channels, voxels, num_bins, soft, include_background != 0, labels,
+      bwd_steps(soft, labels, act, batch, channels, voxels, include_background, moments), 0,
+      moments);
   if (g.lds_bwd > kMaxLds) return ACE_EUNSUPPORTED;
   if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
   if (voxels == 0) return ACE_OK;
@@ -568,9 +586,10 @@ int ace_backward_levels(int levels, const AceBwdLevel* lv, int x_dtype, int64_t 
     const bool moments = use_moments(soft, true, kActSoftmax, batch, channels, v.voxels, num_bins,
                                      include_background);
     if (soft && !moments) return ACE_EUNSUPPORTED;
-    const Geometry g = make_geometry(batch, channels, v.voxels, num_bins, soft,
-                                     include_background != 0, true, env_steps("ACE_BWD_STEPS"), 0,
-                                     moments);
+    const Geometry g = make_geometry(
+        batch, channels, v.voxels, num_bins, soft, include_background != 0, true,
+        bwd_steps(soft, true, kActSoftmax, batch, channels, v.voxels, include_background, moments),
+        0, moments);
     if (g.lds_bwd > kMaxLds) return ACE_EUNSUPPORTED;
     if (nblk + g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
     L.lv[l] = bwd_params(v.x, x_dtype, v.target, true, soft, v.voxels, batch, channels, num_bins,

@@ -2004,13 +2004,21 @@ template <int C, bool SOFT>
 constexpr int fast_bound() {
   return (C <= 4 && !SOFT) ? kFastThreads : kThreads;
 }
+// Backward: at least 4 waves per SIMD (128 VGPRs) for the 16-channel
+// kernel with every channel in the loss, which would otherwise take ~134 and
+// run 3 waves per SIMD (the variant without the background would spill);
+// its grid is sized to match (ace_abi.hip: bwd_steps).
+template <int C, bool SKIP0>
+constexpr int bwd_min_waves() {
+  return (C > 4 && !SKIP0) ? 4 : 1;
+}
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
 __global__ void __launch_bounds__((fast_bound<C, SOFT>())) fwd_kernel_fast(const FwdParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   fwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(P, blockIdx.x, smem);
 }
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
-__global__ void __launch_bounds__(kThreads) bwd_kernel_fast(const BwdParams P) {
+__global__ void __launch_bounds__(kThreads, (bwd_min_waves<C, SKIP0>())) bwd_kernel_fast(const BwdParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   bwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(P, blockIdx.x, smem);
 }
@@ -2046,7 +2054,7 @@ __global__ void __launch_bounds__((fast_bound<C, SOFT>())) fwd_kernel_fast_level
   fwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(L.lv[l], g - L.start[l], smem);
 }
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
-__global__ void __launch_bounds__(kThreads) bwd_kernel_fast_levels(const BwdLevels L) {
+__global__ void __launch_bounds__(kThreads, (bwd_min_waves<C, SKIP0>())) bwd_kernel_fast_levels(const BwdLevels L) {
   extern __shared__ __align__(16) unsigned char smem[];
   const long long g = blockIdx.x;
   const int l = level_of(L.start, L.n, g);
