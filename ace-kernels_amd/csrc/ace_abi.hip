@@ -511,17 +511,13 @@ int ace_forward_levels(int levels, const AceFwdLevel* lv, int x_dtype, int64_t b
     return ACE_EINVAL;
   if (!fast_channels(channels)) return ACE_EUNSUPPORTED;
   const bool soft = binning == ACE_SOFT;
-  // every level in one launch: one block size for all of them -- 1024
-  // threads when each level's geometry allows it, else 256
-  int max_nt = kFastThreads;
-  for (int l = 0; l < levels; ++l) {
+  // every level in one launch, in 256-thread blocks: with the small levels'
+  // many short blocks beside the large one, 1024-thread blocks measured
+  // slower on MI355X (four SegResNetDS levels, hard, HIP graph: 61.6 vs
+  // 57.7 us per step)
+  const int max_nt = kThreads;
+  for (int l = 0; l < levels; ++l)
     if (lv[l].voxels < 0) return ACE_EINVAL;
-    const bool moments = use_moments(soft, true, kActSoftmax, batch, channels, lv[l].voxels,
-                                     num_bins, include_background);
-    const Geometry g = forward_geometry(batch, channels, lv[l].voxels, num_bins, soft,
-                                        include_background, true, kActSoftmax, moments, max_nt);
-    if (g.nt != kFastThreads) max_nt = kThreads;
-  }
   FwdLevels L{};
   L.n = levels;
   L.nt = max_nt;
