@@ -143,6 +143,17 @@ bool fast_forward(bool soft, bool labels, int act, int64_t channels, bool moment
   return act == kActSoftmax && labels && fast_channels(channels) && (!soft || moments);
 }
 
+// Bound of the loss block's wait for another batch epilogue's partial word:
+// kMaxPolls, or ACE_FWD_MAX_POLLS (a test knob: 0 makes the wait give up at
+// once wherever the word has not arrived, the loss NaN, with every kernel
+// still exiting normally).
+int env_max_polls() {
+  const char* v = getenv("ACE_FWD_MAX_POLLS");
+  if (!v) return kMaxPolls;
+  const int n = atoi(v);
+  return n >= 0 && n <= kMaxPolls ? n : kMaxPolls;
+}
+
 // Tuning knob for experiments: largest forward block size (256 or 1024).
 int env_max_threads() {
   const char* v = getenv("ACE_FWD_MAX_THREADS");
@@ -240,6 +251,7 @@ FwdParams fwd_params(const void* x, int x_dtype, const void* target, bool labels
   p.red = reduction;
   p.empty_w = empty_weight;
   p.packed = g.packed ? 1 : 0;
+  p.max_polls = env_max_polls();
   p.pscale = 1.0 / 1073741824.0;  // the generic kernels' sums: 30-bit fixed point
   if (g.fast && !moments) set_fast_bins(p, num_bins, channels);
   if (moments) {

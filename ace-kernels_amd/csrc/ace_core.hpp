@@ -61,6 +61,7 @@ struct FwdParams {
   int epi_all;         // one block runs every batch index's epilogue and the loss
   float empty_w;
   int packed;          // hard binning with labels: final sums W << 32 | G, then P
+  int max_polls;       // bound of the loss block's wait for a partial word (kMaxPolls)
   // fast hard kernels (softmax + class labels, fast_bin): with n = K bins, a
   // probability p is held as q = trunc(p n 2^qs), its bin as q >> qs (q
   // clamped to [qlo, qhi]), and it is "near" an edge when the clamped q lies
@@ -380,6 +381,15 @@ __device__ __forceinline__ void wait_own_writes() {
 // Polls of another block's loss partial word before the loss gives up (NaN):
 // far beyond the few microseconds the other epilogues take.
 constexpr int kMaxPolls = 1 << 20;
+// A partial word the loss block gave up on (no flag bit 32): the late block
+// then finds it instead of zero and clears it, so the workspace is left zero.
+constexpr unsigned long long kAbandoned = 1ull;
+__device__ __forceinline__ unsigned long long cas_dev(unsigned long long* p, unsigned long long expected,
+                                                      unsigned long long desired) {
+  __hip_atomic_compare_exchange_strong(p, &expected, desired, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return expected;  // the word's value before the exchange
+}
 __device__ __forceinline__ int ticket(int* ctr) {
   return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1086,8 +1096,11 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
   // as one word (flag bit 32 | float bits) -- no wait for its own writes, no
   // second ticket -- and the last block polls those words.  The blocks it
   // waits for drew their tickets earlier and run epilogues that wait on
-  // nothing, so the wait ends; it is bounded all the same (kMaxPolls, then
-  // the loss is NaN).
+  // nothing, so the wait ends; it is bounded all the same (P.max_polls, then
+  // the loss is NaN).  A word given up on is marked kAbandoned by a
+  // compare-exchange, which the late block finds when it publishes (also a
+  // compare-exchange) and clears: the workspace is left zero either way, and
+  // the late block runs within the same launch, before any later call.
   int lt = 0;
   int* tc = counter(P, (int64_t)P.B * P.gpb + P.B);
   if (tid == 0 && P.red != kRedNone) lt = ticket(tc);
@@ -1097,7 +1110,9 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
   const bool last = __builtin_amdgcn_readfirstlane(lt) == P.B - 1;
   const float own = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(total)));
   if (!last) {
-    if (tid == 0) store_dev(&P.part[b], (1ull << 32) | (unsigned long long)__float_as_uint(own));
+    if (tid == 0 &&
+        cas_dev(&P.part[b], 0ull, (1ull << 32) | (unsigned long long)__float_as_uint(own)) != 0ull)
+      store_dev(&P.part[b], 0ull);  // the loss block gave up on this word
     return;
   }
   if (tid == 0) __hip_atomic_store(tc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1109,12 +1124,18 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
       v = own;
     } else if (bb < P.B) {
       unsigned long long w = load_dev(&P.part[bb]);
-      for (int n = 0; (w >> 32) == 0 && n < kMaxPolls; ++n) {
+      for (int n = 0; (w >> 32) == 0 && n < P.max_polls; ++n) {
         __builtin_amdgcn_s_sleep(2);
         w = load_dev(&P.part[bb]);
       }
-      v = (w >> 32) ? __uint_as_float((unsigned)w) : __builtin_nanf("");
-      store_dev(&P.part[bb], 0ull);
+      // give up: mark the word abandoned, unless it arrived meanwhile
+      if ((w >> 32) == 0) w = cas_dev(&P.part[bb], 0ull, kAbandoned);
+      if (w >> 32) {
+        v = __uint_as_float((unsigned)w);
+        store_dev(&P.part[bb], 0ull);
+      } else {
+        v = __builtin_nanf("");
+      }
     }
     sum += wave_sum(v);
   }

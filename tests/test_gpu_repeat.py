@@ -52,3 +52,42 @@ def test_repeated_forwards_are_identical_and_leave_the_workspace_zero(binning, b
     stream = torch.cuda.current_stream().cuda_stream
     ws = common._WORKSPACES[("cuda", torch.cuda.current_device(), stream)]
     assert int(torch.count_nonzero(ws)) == 0
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_abandoned_loss_words_leave_the_workspace_zero(monkeypatch, binning) -> None:
+    """The loss block's bounded wait for the other batch epilogues' partial
+    words, forced from the host to give up at once (ACE_FWD_MAX_POLLS=0, read
+    per call; every kernel still exits normally): a loss is then either the
+    right one (every word had arrived) or NaN, the per-bin outputs are
+    unaffected, the workspace is left all zero after every call, and the next
+    normal call gives the exact result again."""
+    gen = torch.Generator().manual_seed(43)
+    b, c, spatial = 65, 2, (16, 16, 8)
+    x = (torch.randn((b, c, *spatial), generator=gen) * 2.0).cuda()
+    y = torch.randint(0, c, (b, 1, *spatial), generator=gen).cuda()
+    cfg = ACEConfig(binning=binning, to_onehot_y=True, activation="softmax")
+    pl = hip.make_plan(x, y, cfg)
+    first = hip.hip_forward(pl, cfg)
+    want_loss, want_coef, want_d = first[0].clone(), first[1].clone(), first[2].clone()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream().cuda_stream
+    ws = common._WORKSPACES[("cuda", torch.cuda.current_device(), stream)]
+    say(f"abandoned loss words {binning}: 50 forwards with ACE_FWD_MAX_POLLS=0")
+    monkeypatch.setenv("ACE_FWD_MAX_POLLS", "0")
+    nan = 0
+    for _ in range(50):
+        loss, coef, d, _, _, _ = hip.hip_forward(pl, cfg)
+        torch.cuda.synchronize()
+        assert torch.equal(coef, want_coef) and torch.equal(d, want_d)
+        if torch.isnan(loss):
+            nan += 1
+        else:
+            assert torch.equal(loss, want_loss)
+        assert int(torch.count_nonzero(ws)) == 0
+    monkeypatch.delenv("ACE_FWD_MAX_POLLS")
+    say(f"abandoned loss words {binning}: {nan} of 50 gave up; normal call")
+    loss, coef, d, _, _, _ = hip.hip_forward(pl, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(loss, want_loss)
+    assert int(torch.count_nonzero(ws)) == 0
