@@ -2200,7 +2200,7 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
     case 2: return LAUNCH<T, 2, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
     case 3: return LAUNCH<T, 3, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
     case 4: return LAUNCH<T, 4, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
-    case 16: return LAUNCH<T, 16, 2, SOFT, RIGHT>(nblk, lds, L, s); \
+    case 16: return LAUNCH<T, 16, 1, SOFT, RIGHT>(nblk, lds, L, s); \
   }                                                               \
   return hipErrorInvalidValue;
 
@@ -2213,7 +2213,7 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
       case 2: return LAUNCH<T, 2, true, 4, SOFT, RIGHT>(g, p, s);                    \
       case 3: return LAUNCH<T, 3, true, 4, SOFT, RIGHT>(g, p, s);                    \
       case 4: return LAUNCH<T, 4, true, 4, SOFT, RIGHT>(g, p, s);                    \
-      case 16: return LAUNCH<T, 16, true, 2, SOFT, RIGHT>(g, p, s);                  \
+      case 16: return LAUNCH<T, 16, true, 1, SOFT, RIGHT>(g, p, s);                  \
     }                                                                                \
   } else {                                                                           \
     switch (v.cmax) {                                                                \

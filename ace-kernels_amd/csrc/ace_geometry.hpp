@@ -24,7 +24,10 @@ constexpr int kFastCopies = 16;            // histogram copies of a 1024-thread 
 
 // Channel variants with a compiled kernel: the kernel keeps C logits of VEC
 // voxels in registers.  EXACT variants fix C at compile time; the others
-// handle any C up to CMAX with uniform guards.
+// handle any C up to CMAX with uniform guards.  C = 16 takes one voxel per
+// lane and step: its forward then holds 107 VGPRs instead of 184 and its
+// backward 81 instead of 128, and on MI355X cfg 4's step went from 104 to
+// 97.6 us (forward 47.2 -> 43.9 us).
 struct Variant {
   int cmax;
   bool exact;
@@ -37,7 +40,7 @@ inline Variant variant_for(int64_t C) {
   if (C == 3) return {3, true, 4};
   if (C == 4) return {4, true, 4};
   if (C <= 8) return {8, false, 4};
-  if (C == 16) return {16, true, 2};
+  if (C == 16) return {16, true, 1};
   if (C <= 16) return {16, false, 4};
   if (C <= 32) return {32, false, 1};
   return {64, false, 1};
