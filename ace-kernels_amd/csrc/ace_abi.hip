@@ -192,9 +192,10 @@ size_t workspace_size(int64_t batch, int64_t channels, int64_t voxels, int num_b
 // Vector steps per backward block: ACE_BWD_STEPS, else make_geometry's
 // choice (~1024 blocks; 512 above 8 channels, where the forward's final-sum
 // atomics set the count) -- except the fast 16-channel backward with every
-// channel in the loss, which holds 4 waves per SIMD (ace_core.hpp:
-// bwd_min_waves) and measured fastest with ~1024 blocks on MI355X (cfg 4:
-// 50.8 vs 57.2 us at 512).
+// channel in the loss, which holds 4 or more waves per SIMD (ace_core.hpp:
+// bwd_min_waves) and measured fastest with ~1024 blocks on MI355X (cfg 4,
+// one voxel per lane: 49.7 us against 53.7 at 512 blocks and 55.2 at ~680;
+// two voxels per lane: 50.8 against 57.2 at 512).
 int bwd_steps(bool soft, bool labels, int act, int64_t batch, int64_t channels, int64_t voxels,
               int include_background, bool moments) {
   const int env = env_steps("ACE_BWD_STEPS");

@@ -2025,10 +2025,10 @@ template <int C, bool SOFT>
 constexpr int fast_bound() {
   return (C <= 4 && !SOFT) ? kFastThreads : kThreads;
 }
-// Backward: at least 4 waves per SIMD (128 VGPRs) for the 16-channel
-// kernel with every channel in the loss, which would otherwise take ~134 and
-// run 3 waves per SIMD (the variant without the background would spill);
-// its grid is sized to match (ace_abi.hip: bwd_steps).
+// Backward: at least 4 waves per SIMD (at most 128 VGPRs) for the
+// 16-channel kernel with every channel in the loss, whose grid is sized for
+// that occupancy (ace_abi.hip: bwd_steps).  At one voxel per lane it takes 81
+// VGPRs and the bound holds by itself; at two it took ~134 without it.
 template <int C, bool SKIP0>
 constexpr int bwd_min_waves() {
   return (C > 4 && !SKIP0) ? 4 : 1;
