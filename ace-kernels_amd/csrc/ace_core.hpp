@@ -2195,13 +2195,14 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
   return launch(kern, nblk, lds, s, L);
 }
 
-#define ACE_LEVELS_SWITCH(LAUNCH, T, SOFT, RIGHT)                 \
-  switch (cmax) {                                                 \
-    case 2: return LAUNCH<T, 2, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
-    case 3: return LAUNCH<T, 3, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
-    case 4: return LAUNCH<T, 4, 4, SOFT, RIGHT>(nblk, lds, L, s);   \
-    case 16: return LAUNCH<T, 16, 1, SOFT, RIGHT>(nblk, lds, L, s); \
-  }                                                               \
+// VEC4: the vector width at C = 4 (the fast hard forward takes 2, make_geometry)
+#define ACE_LEVELS_SWITCH(LAUNCH, T, SOFT, RIGHT, VEC4)               \
+  switch (cmax) {                                                     \
+    case 2: return LAUNCH<T, 2, 4, SOFT, RIGHT>(nblk, lds, L, s);       \
+    case 3: return LAUNCH<T, 3, 4, SOFT, RIGHT>(nblk, lds, L, s);       \
+    case 4: return LAUNCH<T, 4, (VEC4), SOFT, RIGHT>(nblk, lds, L, s);  \
+    case 16: return LAUNCH<T, 16, 1, SOFT, RIGHT>(nblk, lds, L, s);     \
+  }                                                                   \
   return hipErrorInvalidValue;
 
 // Instantiates the per-variant switch for one (element type, binning, right).
@@ -2229,6 +2230,9 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
   template <>                                                                        \
   hipError_t launch_variant_fwd<T, SOFT, RIGHT>(const Geometry& g, const FwdParams& p, \
                                                 hipStream_t s) {                     \
+    if constexpr (!SOFT)                                                             \
+      if (g.var.exact && g.var.cmax == 4 && g.var.vec == 2)                          \
+        return launch_fwd_t<T, 4, true, 2, SOFT, RIGHT>(g, p, s);                    \
     ACE_VARIANT_SWITCH(launch_fwd_t, T, SOFT, RIGHT)                                 \
   }                                                                                  \
   template <>                                                                        \
@@ -2239,12 +2243,12 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
   template <>                                                                        \
   hipError_t launch_levels_fwd<T, SOFT, RIGHT>(int cmax, long long nblk, size_t lds,   \
                                                const FwdLevels& L, hipStream_t s) {  \
-    ACE_LEVELS_SWITCH(launch_fwd_levels_t, T, SOFT, RIGHT)                           \
+    ACE_LEVELS_SWITCH(launch_fwd_levels_t, T, SOFT, RIGHT, (SOFT ? 4 : 2))           \
   }                                                                                  \
   template <>                                                                        \
   hipError_t launch_levels_bwd<T, SOFT, RIGHT>(int cmax, long long nblk, size_t lds,   \
                                                const BwdLevels& L, hipStream_t s) {  \
-    ACE_LEVELS_SWITCH(launch_bwd_levels_t, T, SOFT, RIGHT)                           \
+    ACE_LEVELS_SWITCH(launch_bwd_levels_t, T, SOFT, RIGHT, 4)                        \
   }
 
 }  // namespace ace
