@@ -154,6 +154,16 @@ int env_max_polls() {
   return n >= 0 && n <= kMaxPolls ? n : kMaxPolls;
 }
 
+// Test knob: ACE_FWD_PUBLISH_DELAY sleeps (s_sleep 2 each, at most 2^16)
+// before a batch epilogue publishes its loss partial word, so that a test
+// can make the loss block's bounded wait give up (0 otherwise).
+int env_publish_delay() {
+  const char* v = getenv("ACE_FWD_PUBLISH_DELAY");
+  if (!v) return 0;
+  const int n = atoi(v);
+  return n >= 0 && n <= (1 << 16) ? n : 0;
+}
+
 // Tuning knob for experiments: largest forward block size (256 or 1024).
 int env_max_threads() {
   const char* v = getenv("ACE_FWD_MAX_THREADS");
@@ -253,6 +263,7 @@ FwdParams fwd_params(const void* x, int x_dtype, const void* target, bool labels
   p.empty_w = empty_weight;
   p.packed = g.packed ? 1 : 0;
   p.max_polls = env_max_polls();
+  p.publish_delay = env_publish_delay();
   p.pscale = 1.0 / 1073741824.0;  // the generic kernels' sums: 30-bit fixed point
   if (g.fast && !moments) set_fast_bins(p, num_bins, channels);
   if (moments) {

@@ -62,6 +62,7 @@ struct FwdParams {
   float empty_w;
   int packed;          // hard binning with labels: final sums W << 32 | G, then P
   int max_polls;       // bound of the loss block's wait for a partial word (kMaxPolls)
+  int publish_delay;   // test knob: sleeps before a batch epilogue publishes its word (0)
   // fast hard kernels (softmax + class labels, fast_bin): with n = K bins, a
   // probability p is held as q = trunc(p n 2^qs), its bin as q >> qs (q
   // clamped to [qlo, qhi]), and it is "near" an edge when the clamped q lies
@@ -1110,9 +1111,11 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
   const bool last = __builtin_amdgcn_readfirstlane(lt) == P.B - 1;
   const float own = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(total)));
   if (!last) {
-    if (tid == 0 &&
-        cas_dev(&P.part[b], 0ull, (1ull << 32) | (unsigned long long)__float_as_uint(own)) != 0ull)
-      store_dev(&P.part[b], 0ull);  // the loss block gave up on this word
+    if (tid == 0) {
+      for (int n = 0; n < P.publish_delay; ++n) __builtin_amdgcn_s_sleep(2);
+      if (cas_dev(&P.part[b], 0ull, (1ull << 32) | (unsigned long long)__float_as_uint(own)) != 0ull)
+        store_dev(&P.part[b], 0ull);  // the loss block gave up on this word
+    }
     return;
   }
   if (tid == 0) __hip_atomic_store(tc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

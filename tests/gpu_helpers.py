@@ -101,3 +101,40 @@ def assert_grad_close(grad: torch.Tensor, grad_ref: torch.Tensor, x: torch.Tenso
         )
         assert int(bad.sum()) <= max(1, int(1e-3 * bad.numel())), f"{int(bad.sum())} boundary voxels differ"
     return bad
+
+
+def assert_lowp_grad_close(grad: torch.Tensor, grad_ref: torch.Tensor, x: torch.Tensor,
+                           config: ACEConfig, atol: float = GRAD_ATOL,
+                           truth: torch.Tensor = None) -> torch.Tensor:
+    """dx in bfloat16 / float16 (the logits' type): every element within one
+    unit in the last place of the reference's float32 gradient rounded to
+    that type, plus the north star's atol -- both sides round a float32 value
+    to nearest even, so they differ by a unit only where the two float32
+    values straddle a rounding boundary, and by more only in elements that
+    are small differences of large terms, which atol covers -- except at
+    voxels whose probability is within 1e-6 of a bin boundary, and those
+    rare (the rule of ``assert_grad_close``).  With ``truth`` (the float64
+    gradient) an element also passes when it is at least as close to the
+    truth, rounded to the same type, as the reference is.  Returns the
+    [B, N] mask of voxels that do not pass."""
+    dt = grad.dtype
+    assert dt in (torch.bfloat16, torch.float16), dt
+    mant = 7 if dt == torch.bfloat16 else 10
+    g = grad.detach().cpu().float().flatten(2)
+    r = grad_ref.detach().cpu().float().to(dt).float().flatten(2)
+    # the spacing of dt at |r| (the smallest normal's spacing below it)
+    e = torch.floor(torch.log2(torch.clamp(r.abs(), min=torch.finfo(dt).tiny)))
+    ok = (g - r).abs() <= torch.exp2(e - mant) + atol
+    if truth is not None:
+        t = truth.detach().cpu().double().to(dt).double().flatten(2)
+        ok |= (g.double() - t).abs() <= (r.double() - t).abs()
+    bad = (~ok).any(1)
+    if bad.any():
+        near = near_boundary_voxels(x, config)
+        far = bad & ~near
+        assert not far.any(), (
+            f"{dt} gradient more than one unit from the reference away from bin boundaries at "
+            f"{far.nonzero()[:4].tolist()}: max |diff| {float((g - r).abs().max()):.3e}"
+        )
+        assert int(bad.sum()) <= max(1, int(1e-3 * bad.numel())), f"{int(bad.sum())} boundary voxels differ"
+    return bad

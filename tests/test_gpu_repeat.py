@@ -57,10 +57,12 @@ def test_repeated_forwards_are_identical_and_leave_the_workspace_zero(binning, b
 @pytest.mark.parametrize("binning", ["hard", "soft"])
 def test_abandoned_loss_words_leave_the_workspace_zero(monkeypatch, binning) -> None:
     """The loss block's bounded wait for the other batch epilogues' partial
-    words, forced from the host to give up at once (ACE_FWD_MAX_POLLS=0, read
-    per call; every kernel still exits normally): a loss is then either the
-    right one (every word had arrived) or NaN, the per-bin outputs are
-    unaffected, the workspace is left all zero after every call, and the next
+    words, forced from the host to give up: ACE_FWD_MAX_POLLS=0 (no polls)
+    and ACE_FWD_PUBLISH_DELAY (the other epilogues sleep ~0.1 ms before they
+    publish), both read per call; every kernel still exits normally.  A loss
+    is then NaN (or the right one, if every word had arrived), the per-bin
+    outputs are unaffected, the late words find their abandoned marks and
+    clear them, so the workspace is all zero after every call, and the next
     normal call gives the exact result again."""
     gen = torch.Generator().manual_seed(43)
     b, c, spatial = 65, 2, (16, 16, 8)
@@ -73,8 +75,9 @@ def test_abandoned_loss_words_leave_the_workspace_zero(monkeypatch, binning) -> 
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream().cuda_stream
     ws = common._WORKSPACES[("cuda", torch.cuda.current_device(), stream)]
-    say(f"abandoned loss words {binning}: 50 forwards with ACE_FWD_MAX_POLLS=0")
+    say(f"abandoned loss words {binning}: 50 forwards with no polls and delayed words")
     monkeypatch.setenv("ACE_FWD_MAX_POLLS", "0")
+    monkeypatch.setenv("ACE_FWD_PUBLISH_DELAY", "2000")
     nan = 0
     for _ in range(50):
         loss, coef, d, _, _, _ = hip.hip_forward(pl, cfg)
@@ -86,7 +89,9 @@ def test_abandoned_loss_words_leave_the_workspace_zero(monkeypatch, binning) -> 
             assert torch.equal(loss, want_loss)
         assert int(torch.count_nonzero(ws)) == 0
     monkeypatch.delenv("ACE_FWD_MAX_POLLS")
+    monkeypatch.delenv("ACE_FWD_PUBLISH_DELAY")
     say(f"abandoned loss words {binning}: {nan} of 50 gave up; normal call")
+    assert nan > 0  # the give-up path ran
     loss, coef, d, _, _, _ = hip.hip_forward(pl, cfg)
     torch.cuda.synchronize()
     assert torch.equal(loss, want_loss)
