@@ -17,7 +17,11 @@ this package can be put beside a row of the reference's harness:
   allocated afterwards;
 - accuracy (untimed): loss and gradient against a trusted implementation on
   the same input (``|L - L_ref| / |L_ref|``, ``max|g - g_ref| / max|g_ref|``,
-  ``||g - g_ref|| / ||g_ref||``) and against a float64 truth.
+  ``||g - g_ref|| / ||g_ref||``) and against a float64 truth;
+- HBM traffic (opt-in, ``counters=True``): bytes the library's kernels read
+  from and write to HBM per call, from rocprofv3's FETCH_SIZE / WRITE_SIZE
+  counters calibrated by a copy of known size (``ace_kernels.counters``), and
+  their ratio to the ideal bytes.
 
 Which implementation is trusted is the caller's choice: ``compute_reference``
 calls whatever the registry holds under ``ref_impl`` / ``truth_impl`` (this
@@ -96,6 +100,11 @@ class Row(BaseModel):
     grad_l2_err: Optional[float] = None
     grad_l2_err_truth: Optional[float] = None
     ref_grad_l2_err_truth: Optional[float] = None
+    # rocprofv3 counters (ace_kernels.counters), per call, library kernels only
+    hbm_read_bytes: Optional[int] = None
+    hbm_write_bytes: Optional[int] = None
+    hbm_bytes_per_ideal: Optional[float] = None
+    counted_kernels_per_call: Optional[int] = None
 
 
 # ---------------------------------------------------------------- inputs
@@ -221,6 +230,11 @@ class Reference:
     ref_loss_err_truth: Optional[float] = None
     ref_grad_err_truth: Optional[float] = None
     ref_grad_l2_err_truth: Optional[float] = None
+    # rocprofv3 counters (ace_kernels.counters), per call, library kernels only
+    hbm_read_bytes: Optional[int] = None
+    hbm_write_bytes: Optional[int] = None
+    hbm_bytes_per_ideal: Optional[float] = None
+    counted_kernels_per_call: Optional[int] = None
 
 
 def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
@@ -361,11 +375,31 @@ def release_memory() -> None:
 # ---------------------------------------------------------------- one row
 
 
+def fill_counters(row: Row, impl: str, shape: ShapeSpec, config: ACEConfig, mode: Mode,
+                  dtype: torch.dtype, seed: int, calls: int = 10) -> None:
+    """The row's HBM traffic columns from two rocprofv3 counter runs of the
+    same case in child processes (ace_kernels.counters)."""
+    from ace_kernels import counters
+
+    case = counters.CaseArgs(impl=impl, config=config.model_dump_json(), batch=shape.batch,
+                             channels=shape.channels, spatial=tuple(shape.spatial),
+                             logit_scale=shape.logit_scale, target_bias=shape.target_bias,
+                             mode=mode, dtype=str(dtype).replace("torch.", ""), seed=seed,
+                             calls=calls)
+    tr = counters.collect(case)
+    row.hbm_read_bytes = round(tr.read_bytes)
+    row.hbm_write_bytes = round(tr.write_bytes)
+    row.hbm_bytes_per_ideal = tr.total_bytes / row.ideal_bytes
+    row.counted_kernels_per_call = tr.dispatches
+
+
 def measure_case(impl: str, shape: ShapeSpec, config: ACEConfig, mode: Mode, *,
                  cuda_graph: bool = False, warmup: int = 3, reps: int = 10, seed: int = 0,
                  reference: Optional[Reference] = None, dtype: torch.dtype = torch.float32,
-                 peak_gbps: float = PEAK_HBM_GBPS) -> Row:
-    """measure.py:280-360 for one case on the current HIP device."""
+                 peak_gbps: float = PEAK_HBM_GBPS, counters: bool = False) -> Row:
+    """measure.py:280-360 for one case on the current HIP device; with
+    ``counters`` also the HBM traffic columns (not for graph rows; a counter
+    failure is recorded in ``error`` and leaves the timing columns)."""
     x, y = make_inputs(shape, config, "cuda", seed)
     x = x.to(dtype).requires_grad_(True)
     in_bytes = x.numel() * x.element_size()
@@ -407,6 +441,12 @@ def measure_case(impl: str, shape: ShapeSpec, config: ACEConfig, mode: Mode, *,
             if reference is not None and not cuda_graph:
                 del fn
                 check_output(row, impl, x, y, config, reference)
+            if counters and not cuda_graph:
+                try:
+                    fill_counters(row, impl, shape, config, mode, dtype, seed)
+                except Exception as exc:  # noqa: BLE001 -- recorded in the row
+                    row.error = ("counters: " + "".join(
+                        traceback.format_exception_only(exc)).strip())[:500]
     except torch.OutOfMemoryError as exc:
         row.status, row.error = "oom", str(exc).splitlines()[0][:500]
     except Exception as exc:  # noqa: BLE001 -- recorded in the row
@@ -429,6 +469,8 @@ def main(argv: Optional[List[str]] = None) -> int:
     ap.add_argument("--modes", default="fwd,fwd_bwd")
     ap.add_argument("--graph", action="store_true", help="also the HIP-graph rows")
     ap.add_argument("--reps", type=int, default=10)
+    ap.add_argument("--counters", action="store_true",
+                    help="also HBM read / write bytes per call (two rocprofv3 counter runs per row)")
     args = ap.parse_args(argv)
     import ace_kernels  # noqa: F401 -- registers the implementations
 
@@ -439,7 +481,8 @@ def main(argv: Optional[List[str]] = None) -> int:
             for impl in args.impls.split(","):
                 for mode in args.modes.split(","):
                     for graph in ((False, True) if args.graph else (False,)):
-                        row = measure_case(impl, shape, cfg, mode, cuda_graph=graph, reps=args.reps)
+                        row = measure_case(impl, shape, cfg, mode, cuda_graph=graph, reps=args.reps,
+                                           counters=args.counters)
                         print(json.dumps(row.model_dump()), flush=True)
     return 0
 

@@ -27,8 +27,15 @@ REFERENCE_ROW_FIELDS = [
 ]
 
 
+# This package's rocprofv3 counter columns, after the reference's fields.
+COUNTER_FIELDS = ["hbm_read_bytes", "hbm_write_bytes", "hbm_bytes_per_ideal",
+                  "counted_kernels_per_call"]
+
+
 def test_row_schema_matches_the_reference() -> None:
-    assert list(m.Row.model_fields) == REFERENCE_ROW_FIELDS
+    fields = list(m.Row.model_fields)
+    assert fields[:len(REFERENCE_ROW_FIELDS)] == REFERENCE_ROW_FIELDS
+    assert fields[len(REFERENCE_ROW_FIELDS):] == COUNTER_FIELDS
 
 
 def test_ideal_bytes_and_floors() -> None:
