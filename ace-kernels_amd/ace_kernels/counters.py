@@ -12,8 +12,8 @@ takes at most 4 TCC counters and FETCH_SIZE alone uses 3):
 
 Each run is a child process, ``rocprofv3 --pmc <counter> -- python -m
 ace_kernels.counters --child <case>``, that rebuilds the case from its
-arguments, calls it ``calls`` times, then copies the calibration tensor
-``calls`` times.  The per-call bytes are the counters of every dispatch whose
+arguments (or takes a benchmark configuration's inputs), calls it ``calls``
+times, then copies the calibration tensor ``calls`` times.  The per-call bytes are the counters of every dispatch whose
 kernel name contains ``kernel_filter`` (the library's kernels by default),
 summed and divided by ``calls``.
 """
@@ -53,6 +53,7 @@ class CaseArgs:
     dtype: str  # torch dtype name, e.g. "float32"
     seed: int
     calls: int = 10
+    workload: int = 0  # > 0: the inputs and config of benchmark configuration `workload`
 
     def to_argv(self) -> List[str]:
         return ["--child", json.dumps(asdict(self))]
@@ -178,11 +179,19 @@ def _run_child(case: CaseArgs) -> int:
     from ace_kernels.config import ACEConfig
     from ace_kernels.measure import ShapeSpec, make_inputs, step_fn
 
-    cfg = ACEConfig.model_validate_json(case.config)
-    shape = ShapeSpec("counted", case.batch, case.channels, case.spatial, case.logit_scale,
-                      case.target_bias)
-    x, y = make_inputs(shape, cfg, "cuda", case.seed)
-    x = x.to(getattr(torch, case.dtype)).requires_grad_(True)
+    if case.workload > 0:
+        from ace_kernels.workloads import workload
+
+        wl = workload(case.workload)
+        cfg = wl.config
+        x, y = wl.make("cuda")
+        x = x.requires_grad_(True)
+    else:
+        cfg = ACEConfig.model_validate_json(case.config)
+        shape = ShapeSpec("counted", case.batch, case.channels, case.spatial, case.logit_scale,
+                          case.target_bias)
+        x, y = make_inputs(shape, cfg, "cuda", case.seed)
+        x = x.to(getattr(torch, case.dtype)).requires_grad_(True)
     fn = step_fn(case.impl, x, y, cfg, case.mode)  # type: ignore[arg-type]
     # no warm-up call: every call of the case is counted and divided by calls
     for _ in range(case.calls):

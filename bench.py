@@ -22,10 +22,14 @@ launch / its mean duration over the timed launches (cold cache; HIP events
 that the kernel's dispatch stamps as it starts and ends, through
 ``ace_set_launch_events``, so they agree with rocprofv3's kernel durations;
 events recorded on the stream around the same launches, which add the
-dispatch gap after the flush, are reported beside them).  ``traffic`` is read
-from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-(``profiles/traffic_cfg2.json``) when it was measured on the current kernel
-sources, else null.  ``cpu_baseline`` times the reference algorithm (restated
+dispatch gap after the flush, are reported beside them).  ``traffic`` is
+measured in the same run, after the timings: two rocprofv3 counter runs
+(FETCH_SIZE, then WRITE_SIZE) of the first workload's loss in child
+processes, scaled by a copy of known size (``ace_kernels.counters``).  If
+that fails (or with ``--no-counters``, which profiling runs under rocprofv3
+use) it is read from the committed summary (``profiles/traffic_cfg2.json``)
+when that was measured on the current kernel sources, else null;
+``traffic_source`` says which.  ``cpu_baseline`` times the reference algorithm (restated
 in ``oracle/``) fwd+bwd on the host CPU: configuration 2 (``value``), and
 configuration 1 hard and soft and configuration 3 as ``rows``.
 
@@ -483,6 +487,32 @@ def _traffic(kernel: str):
         return None
 
 
+def live_traffic(idx: int, kernel: str):
+    """HBM bytes per launch of ``kernel`` ("ace_fwd" / "ace_bwd") on workload
+    ``idx``, measured now: two rocprofv3 counter runs of the workload's loss
+    (forward only for the forward kernel) in child processes, calibrated by a
+    256 MiB copy (``ace_kernels.counters``).  None when rocprofv3 is missing
+    or a run fails or takes over a minute."""
+    from ace_kernels import counters
+    from ace_kernels.workloads import workload
+
+    wl = workload(idx)
+    case = counters.CaseArgs(
+        impl="hip_mi355x", config=wl.config.model_dump_json(), batch=wl.batch,
+        channels=wl.channels, spatial=tuple(wl.spatial), logit_scale=wl.scale, target_bias=0.0,
+        mode="fwd" if kernel == "ace_fwd" else "fwd_bwd", dtype=str(wl.dtype).replace("torch.", ""),
+        seed=wl.seed, workload=idx)
+    filt = "ace::fwd_kernel" if kernel == "ace_fwd" else "ace::bwd_kernel"
+    try:
+        tr = counters.collect(case, timeout=60.0, kernel_filter=filt)
+    except Exception as exc:  # noqa: BLE001 -- reported, then the committed summary is used
+        log(f"live traffic failed: {type(exc).__name__}: {str(exc)[:300]}")
+        return None
+    log(f"live traffic {wl.name} {kernel}: read {tr.read_bytes:.0f} B, write {tr.write_bytes:.0f} B "
+        f"(fetch x{tr.fetch_scale:.4f}, write x{tr.write_scale:.4f})")
+    return tr
+
+
 COPY_KIB = 262144.0  # profile_kernels' calibration copy: 256 MiB read and 256 MiB written
 
 
@@ -580,6 +610,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU baseline row")
     ap.add_argument("--workloads", default="2,3,4,5", help="benchmark workloads (first = value)")
     ap.add_argument("--no-deepsup", action="store_true", help="skip the deep-supervision steps")
+    ap.add_argument("--no-counters", action="store_true",
+                    help="no live rocprofv3 traffic runs (for runs under a profiler)")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="LAUNCHES",
                     help="only launch the kernels LAUNCHES times each (for rocprofv3)")
     ap.add_argument("--summarize-profiles", nargs="+", metavar="DIR",
@@ -625,6 +657,17 @@ def main() -> int:
     main_r = results[0]
     dom = main_r["dominant"]
     achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
+    traffic, traffic_source, traffic_rw = None, None, None
+    if not args.no_counters:
+        log(f"live traffic of {dom['kernel']} (two rocprofv3 counter runs)")
+        tr = live_traffic(int(args.workloads.split(",")[0]), dom["kernel"])
+        if tr is not None:
+            traffic, traffic_source = tr.total_bytes, "live rocprofv3 FETCH_SIZE + WRITE_SIZE"
+            traffic_rw = {"read": tr.read_bytes, "write": tr.write_bytes,
+                          "fetch_scale": tr.fetch_scale, "write_scale": tr.write_scale}
+    if traffic is None:
+        traffic = _traffic(dom["kernel"])
+        traffic_source = TRAFFIC_FILE.name if traffic is not None else None
     line = {
         "metric": METRIC,
         "value": main_r["eager_ms"]["p50"],
@@ -658,7 +701,9 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBPS,
-            "traffic": _traffic(dom["kernel"]),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
+            "traffic_rw": traffic_rw,
             "bytes_per_launch": dom["bytes"],
             "bytes_per_voxel": dom["bytes_per_voxel"],
             "ms_mean": dom["ms"],
