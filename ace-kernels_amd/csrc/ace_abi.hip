@@ -87,6 +87,12 @@ int env_copies() {
 
 size_t elem_size(int dtype) { return dtype == ACE_F32 ? 4 : 2; }
 
+// Bytes of the targets: int64 class labels [B, N] or float32 one-hot [B, C, N].
+size_t target_bytes(bool labels, int64_t batch, int64_t channels, int64_t voxels) {
+  return labels ? 8 * (size_t)batch * (size_t)voxels
+                : 4 * (size_t)batch * (size_t)channels * (size_t)voxels;
+}
+
 bool aligned_to(const void* p, size_t a) {
   return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }
@@ -326,6 +332,8 @@ BwdParams bwd_params(const void* x, int x_dtype, const void* target, bool labels
   p.d = diff;
   p.jac = jac;
   p.go = grad_output;
+  p.stream = stream_problem(es * (size_t)batch * (size_t)channels * (size_t)voxels,
+                            target_bytes(labels, batch, channels, voxels)) ? 1 : 0;
 
   return p;
 }

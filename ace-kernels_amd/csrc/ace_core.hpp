@@ -114,6 +114,7 @@ struct BwdParams {
   const float* d;
   const float* jac;
   const float* go;
+  int stream;          // streaming (nontemporal) gradient stores: stream_problem
 };
 
 // ------------------------------------------------------------ conversions
@@ -140,6 +141,13 @@ template <> struct RawVec<8> { using type = uint2; };
 template <> struct RawVec<4> { using type = unsigned int; };
 template <> struct RawVec<2> { using type = unsigned short; };
 
+// The same widths as clang vector types, which the nontemporal load and
+// store builtins take (global_load / global_store with the nt bit).
+typedef unsigned int xu32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int xu32x2 __attribute__((ext_vector_type(2)));
+template <int BYTES> struct XVec { using type = typename RawVec<BYTES>::type; };
+template <> struct XVec<16> { using type = xu32x4; };
+template <> struct XVec<8> { using type = xu32x2; };
 // VEC consecutive elements from an address aligned to VEC * sizeof(T).
 template <typename T, int VEC>
 __device__ __forceinline__ void load_vec(const T* __restrict__ p, float (&out)[VEC]) {
@@ -160,6 +168,26 @@ __device__ __forceinline__ void store_vec(T* __restrict__ p, const float (&in)[V
   R raw;
   __builtin_memcpy(&raw, vals, sizeof(R));
   *reinterpret_cast<R*>(p) = raw;
+}
+
+// store_vec with a nontemporal store (streamed past the caches).
+template <typename T, int VEC>
+__device__ __forceinline__ void store_vec_nt(T* __restrict__ p, const float (&in)[VEC]) {
+  using R = typename XVec<sizeof(T) * VEC>::type;
+  T vals[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) vals[j] = from_f32<T>(in[j]);
+  R raw;
+  __builtin_memcpy(&raw, vals, sizeof(R));
+  __builtin_nontemporal_store(raw, reinterpret_cast<R*>(p));
+}
+// A gradient store: nontemporal for streaming problems (stream_problem).
+template <typename T, int VEC, bool NT>
+__device__ __forceinline__ void store_dx(T* __restrict__ p, const float (&in)[VEC]) {
+  if constexpr (NT)
+    store_vec_nt<T, VEC>(p, in);
+  else
+    store_vec<T, VEC>(p, in);
 }
 
 // Class index of an int64 label if it names a channel in [0, C), else -1.
@@ -1412,22 +1440,49 @@ struct FastTile {
   long long lab[VEC];  // raw int64 labels, converted when used
 };
 
-template <typename T, int C, int VEC>
+// load_vec with a nontemporal load.
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec_nt(const T* __restrict__ p, float (&out)[VEC]) {
+  using R = typename XVec<sizeof(T) * VEC>::type;
+  const R raw = __builtin_nontemporal_load(reinterpret_cast<const R*>(p));
+  T vals[VEC];
+  __builtin_memcpy(vals, &raw, sizeof(R));
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) out[j] = to_f32<T>(vals[j]);
+}
+// One tile's logits and labels; NTX / NTL: nontemporal loads of the logits
+// / labels (data that no later kernel of the step reads from the cache).
+template <typename T, int C, int VEC, bool NTX = false, bool NTL = false>
 __device__ __forceinline__ void fast_load(FastTile<C, VEC>& t, const T* const (&xr)[C],
                                           const long long* lr, uint32_t v, bool with_labels) {
 #pragma unroll
-  for (int c = 0; c < C; ++c) load_vec<T, VEC>(xr[c] + v, t.x[c]);
+  for (int c = 0; c < C; ++c) {
+    if constexpr (NTX) load_vec_nt<T, VEC>(xr[c] + v, t.x[c]);
+    else load_vec<T, VEC>(xr[c] + v, t.x[c]);
+  }
   if (with_labels) {
     if constexpr (VEC % 2 == 0) {
 #pragma unroll
       for (int j = 0; j < VEC; j += 2) {
-        const longlong2 q = *reinterpret_cast<const longlong2*>(lr + v + j);
-        t.lab[j] = q.x;
-        t.lab[j + 1] = q.y;
+        if constexpr (NTL) {
+          typedef long long xi64x2 __attribute__((ext_vector_type(2)));
+          const xi64x2 q = __builtin_nontemporal_load(reinterpret_cast<const xi64x2*>(lr + v + j));
+          t.lab[j] = q.x;
+          t.lab[j + 1] = q.y;
+        } else {
+          const longlong2 q = *reinterpret_cast<const longlong2*>(lr + v + j);
+          t.lab[j] = q.x;
+          t.lab[j + 1] = q.y;
+        }
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) t.lab[j] = lr[v + j];
+      for (int j = 0; j < VEC; ++j) {
+        if constexpr (NTL)
+          t.lab[j] = __builtin_nontemporal_load(lr + v + j);
+        else
+          t.lab[j] = lr[v + j];
+      }
     }
   }
 }
@@ -1786,8 +1841,8 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
 #pragma unroll
     for (int c = 0; c < C; ++c) px[c] = pipe ? xr[c] : reinterpret_cast<const T*>(g_dummy_src);
     const long long* pl = pipe ? lr_ : reinterpret_cast<const long long*>(g_dummy_src);
-    fast_load<T, C, VEC>(ta, px, pl, pipe ? at(0) : 0u, true);
-    fast_load<T, C, VEC>(tb, px, pl, pipe ? at(1) : 0u, true);
+    fast_load<T, C, VEC, false, !SOFT>(ta, px, pl, pipe ? at(0) : 0u, true);
+    fast_load<T, C, VEC, false, !SOFT>(tb, px, pl, pipe ? at(1) : 0u, true);
   }
   // soft: the bucket table scaled by 2^m like softmax_fixed's probabilities;
   // hard: as given (the exact path's bucket_unit)
@@ -1811,9 +1866,9 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
     int i = 0;
     for (; i + 2 < nsteps; i += 2) {
       fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, P, K, lsh, hb, words);
-      fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), true);
+      fast_load<T, C, VEC, false, !SOFT>(ta, xr, lr_, at(i + 2), true);
       fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, P, K, lsh, hb, words);
-      fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), true);
+      fast_load<T, C, VEC, false, !SOFT>(tb, xr, lr_, at(i + 3), true);
     }
     fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, P, K, lsh, hb, words);
     if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, P, K, lsh, hb, words);
@@ -1821,7 +1876,7 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
   // remaining full vectors (not every thread has one), then single voxels
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
-    fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, true);
+    fast_load<T, C, VEC, false, !SOFT>(t, xr, lr_, (uint32_t)v, true);
     fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, P, K, lsh, hb, words);
   }
   for (int v = nfull + tid; v < nvox; v += nt) {
@@ -1899,7 +1954,7 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
   }
 }
 
-template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0, bool STREAM>
 __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t blk,
                                               unsigned char* smem) {
   float* tabs = reinterpret_cast<float*>(smem);
@@ -1988,20 +2043,20 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
     for (; i + 2 < nsteps; i += 2) {
       fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, sab, scoef, sg, K);
 #pragma unroll
-      for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i), ta.x[c]);
+      for (int c = 0; c < C; ++c) store_dx<T, VEC, STREAM>(dr[c] + at(i), ta.x[c]);
       fast_load<T, C, VEC>(ta, xr, lr_, at(i + 2), SOFT);
       fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, sab, scoef, sg, K);
 #pragma unroll
-      for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i + 1), tb.x[c]);
+      for (int c = 0; c < C; ++c) store_dx<T, VEC, STREAM>(dr[c] + at(i + 1), tb.x[c]);
       fast_load<T, C, VEC>(tb, xr, lr_, at(i + 3), SOFT);
     }
     fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, sab, scoef, sg, K);
 #pragma unroll
-    for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i), ta.x[c]);
+    for (int c = 0; c < C; ++c) store_dx<T, VEC, STREAM>(dr[c] + at(i), ta.x[c]);
     if (i + 1 < nsteps) {
       fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, sab, scoef, sg, K);
 #pragma unroll
-      for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + at(i + 1), tb.x[c]);
+      for (int c = 0; c < C; ++c) store_dx<T, VEC, STREAM>(dr[c] + at(i + 1), tb.x[c]);
     }
   }
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
@@ -2009,7 +2064,7 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
     fast_load<T, C, VEC>(t, xr, lr_, (uint32_t)v, SOFT);
     fast_backward<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, sab, scoef, sg, K);
 #pragma unroll
-    for (int c = 0; c < C; ++c) store_vec<T, VEC>(dr[c] + v, t.x[c]);
+    for (int c = 0; c < C; ++c) store_dx<T, VEC, STREAM>(dr[c] + v, t.x[c]);
   }
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     FastTile<C, 1> t;
@@ -2041,10 +2096,12 @@ __global__ void __launch_bounds__((fast_bound<C, SOFT>())) fwd_kernel_fast(const
   extern __shared__ __align__(16) unsigned char smem[];
   fwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(P, blockIdx.x, smem);
 }
-template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
+// STREAM: the problem's logits, targets and gradient exceed the last-level
+// cache (stream_problem): the gradient is written with nontemporal stores.
+template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0, bool STREAM>
 __global__ void __launch_bounds__(kThreads, (bwd_min_waves<C, SKIP0>())) bwd_kernel_fast(const BwdParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
-  bwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(P, blockIdx.x, smem);
+  bwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0, STREAM>(P, blockIdx.x, smem);
 }
 
 // Several problems of one configuration in one launch (the levels of a
@@ -2082,7 +2139,7 @@ __global__ void __launch_bounds__(kThreads, (bwd_min_waves<C, SKIP0>())) bwd_ker
   extern __shared__ __align__(16) unsigned char smem[];
   const long long g = blockIdx.x;
   const int l = level_of(L.start, L.n, g);
-  bwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0>(L.lv[l], g - L.start[l], smem);
+  bwd_fast_body<T, C, VEC, SOFT, RIGHT, SKIP0, false>(L.lv[l], g - L.start[l], smem);
 }
 
 // ------------------------------------------------------------ launchers
@@ -2159,9 +2216,14 @@ hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) 
   auto kern = bwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
   if constexpr (has_fast<CMAX, EXACT>()) {
     // the hard gradient reads no targets: any target layout takes the fast path
-    if (prm.act == kActSoftmax && (!SOFT || (prm.tk == kTgtLabels && g.moments)))
-      kern = prm.off ? bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true>
-                     : bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false>;
+    if (prm.act == kActSoftmax && (!SOFT || (prm.tk == kTgtLabels && g.moments))) {
+      if (prm.stream)
+        kern = prm.off ? bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true, true>
+                       : bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false, true>;
+      else
+        kern = prm.off ? bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true, false>
+                       : bwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false, false>;
+    }
   }
   if (g.lds_bwd > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

@@ -84,6 +84,22 @@ constexpr EpiLayout epi_layout(int ck, int cl, int nb, bool moments) {
 }
 constexpr int kMaxEpiRows = 16;  // C' up to which a single batch index's epilogue sums the loss
 
+// A problem streams when its logits, targets and gradient exceed
+// kStreamBytes, 7/8 of MI355X's 256 MB last-level cache: the backward then
+// writes the gradient with nontemporal stores, so that the gradient does not
+// displace the logits that the forward left in that cache and the backward
+// reads.  Below it the gradient's lines are written back from the cache
+// after the kernel.  Separately, the hard forward reads the class labels
+// with nontemporal loads at every size (the hard backward does not read
+// them).  On MI355X, eager fwd+bwd step: cfg 4 (285 MB) -6 us with the
+// streaming stores; cfg 2 (168 MB) -1.2 to -2.5 us with the label loads,
+// +0.5 us with streaming stores.  Nontemporal logit loads in the forward
+// too made cfg 4's step 10 us slower instead.
+constexpr size_t kStreamBytes = (size_t)224 << 20;
+inline bool stream_problem(size_t x_bytes, size_t target_bytes) {
+  return 2 * x_bytes + target_bytes > kStreamBytes;
+}
+
 // Channel counts served by the fast (softmax + class-index labels) kernels.
 inline bool fast_channels(int64_t C) { return C == 2 || C == 3 || C == 4 || C == 16; }
 
