@@ -141,8 +141,8 @@ template <> struct RawVec<8> { using type = uint2; };
 template <> struct RawVec<4> { using type = unsigned int; };
 template <> struct RawVec<2> { using type = unsigned short; };
 
-// The same widths as clang vector types, which the nontemporal load and
-// store builtins take (global_load / global_store with the nt bit).
+// The same widths as clang vector types, which the nontemporal store builtin
+// takes (global_store with the nt bit).
 typedef unsigned int xu32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int xu32x2 __attribute__((ext_vector_type(2)));
 template <int BYTES> struct XVec { using type = typename RawVec<BYTES>::type; };
@@ -1440,26 +1440,13 @@ struct FastTile {
   long long lab[VEC];  // raw int64 labels, converted when used
 };
 
-// load_vec with a nontemporal load.
-template <typename T, int VEC>
-__device__ __forceinline__ void load_vec_nt(const T* __restrict__ p, float (&out)[VEC]) {
-  using R = typename XVec<sizeof(T) * VEC>::type;
-  const R raw = __builtin_nontemporal_load(reinterpret_cast<const R*>(p));
-  T vals[VEC];
-  __builtin_memcpy(vals, &raw, sizeof(R));
-#pragma unroll
-  for (int j = 0; j < VEC; ++j) out[j] = to_f32<T>(vals[j]);
-}
-// One tile's logits and labels; NTX / NTL: nontemporal loads of the logits
-// / labels (data that no later kernel of the step reads from the cache).
-template <typename T, int C, int VEC, bool NTX = false, bool NTL = false>
+// One tile's logits and labels; NTL: nontemporal loads of the labels (the
+// hard forward: no later kernel of the step reads them, stream_problem).
+template <typename T, int C, int VEC, bool NTL = false>
 __device__ __forceinline__ void fast_load(FastTile<C, VEC>& t, const T* const (&xr)[C],
                                           const long long* lr, uint32_t v, bool with_labels) {
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
-    if constexpr (NTX) load_vec_nt<T, VEC>(xr[c] + v, t.x[c]);
-    else load_vec<T, VEC>(xr[c] + v, t.x[c]);
-  }
+  for (int c = 0; c < C; ++c) load_vec<T, VEC>(xr[c] + v, t.x[c]);
   if (with_labels) {
     if constexpr (VEC % 2 == 0) {
 #pragma unroll
@@ -1841,8 +1828,8 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
 #pragma unroll
     for (int c = 0; c < C; ++c) px[c] = pipe ? xr[c] : reinterpret_cast<const T*>(g_dummy_src);
     const long long* pl = pipe ? lr_ : reinterpret_cast<const long long*>(g_dummy_src);
-    fast_load<T, C, VEC, false, !SOFT>(ta, px, pl, pipe ? at(0) : 0u, true);
-    fast_load<T, C, VEC, false, !SOFT>(tb, px, pl, pipe ? at(1) : 0u, true);
+    fast_load<T, C, VEC, !SOFT>(ta, px, pl, pipe ? at(0) : 0u, true);
+    fast_load<T, C, VEC, !SOFT>(tb, px, pl, pipe ? at(1) : 0u, true);
   }
   // soft: the bucket table scaled by 2^m like softmax_fixed's probabilities;
   // hard: as given (the exact path's bucket_unit)
@@ -1866,9 +1853,9 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
     int i = 0;
     for (; i + 2 < nsteps; i += 2) {
       fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, P, K, lsh, hb, words);
-      fast_load<T, C, VEC, false, !SOFT>(ta, xr, lr_, at(i + 2), true);
+      fast_load<T, C, VEC, !SOFT>(ta, xr, lr_, at(i + 2), true);
       fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, P, K, lsh, hb, words);
-      fast_load<T, C, VEC, false, !SOFT>(tb, xr, lr_, at(i + 3), true);
+      fast_load<T, C, VEC, !SOFT>(tb, xr, lr_, at(i + 3), true);
     }
     fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(ta, tab, P, K, lsh, hb, words);
     if (i + 1 < nsteps) fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(tb, tab, P, K, lsh, hb, words);
@@ -1876,7 +1863,7 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
   // remaining full vectors (not every thread has one), then single voxels
   for (int v = nsteps * stride + tid * VEC; v < nfull; v += stride) {
     FastTile<C, VEC> t;
-    fast_load<T, C, VEC, false, !SOFT>(t, xr, lr_, (uint32_t)v, true);
+    fast_load<T, C, VEC, !SOFT>(t, xr, lr_, (uint32_t)v, true);
     fast_accumulate<C, VEC, SOFT, RIGHT, SKIP0>(t, tab, P, K, lsh, hb, words);
   }
   for (int v = nfull + tid; v < nvox; v += nt) {
