@@ -87,3 +87,37 @@ def test_row_counter_columns_default_to_none() -> None:
                 target_bytes=4096, ideal_bytes=12288)
     assert row.hbm_read_bytes is None and row.hbm_write_bytes is None
     assert row.hbm_bytes_per_ideal is None and row.counted_kernels_per_call is None
+
+
+def test_bench_live_traffic_case_and_fallback(monkeypatch) -> None:
+    """bench.py's live traffic asks for the dominant kernel of the workload's
+    loss (forward only for the forward kernel) and returns None when the
+    counter runs fail, so that the committed summary is used instead."""
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parent.parent
+    sys.path.insert(0, str(root))
+    import bench
+
+    seen = []
+
+    def fake_collect(case, timeout=120.0, kernel_filter=ct.KERNEL_FILTER):
+        seen.append((case, kernel_filter))
+        return ct.Traffic(read_bytes=1.0, write_bytes=2.0, fetch_kib=0.0, write_kib=0.0,
+                          fetch_scale=2.0, write_scale=1.0, dispatches=1)
+
+    monkeypatch.setattr(ct, "collect", fake_collect)
+    tr = bench.live_traffic(2, "ace_fwd")
+    assert tr.total_bytes == 3.0
+    case, filt = seen[-1]
+    assert case.workload == 2 and case.mode == "fwd" and filt == "ace::fwd_kernel"
+    bench.live_traffic(4, "ace_bwd")
+    case, filt = seen[-1]
+    assert case.workload == 4 and case.mode == "fwd_bwd" and filt == "ace::bwd_kernel"
+
+    def failing_collect(*args, **kwargs):
+        raise RuntimeError("rocprofv3 --pmc FETCH_SIZE failed")
+
+    monkeypatch.setattr(ct, "collect", failing_collect)
+    assert bench.live_traffic(2, "ace_fwd") is None
