@@ -569,6 +569,8 @@ int ace_forward_levels(int levels, const AceFwdLevel* lv, int x_dtype, int64_t b
     const Geometry g = forward_geometry(batch, channels, v.voxels, num_bins, soft,
                                         include_background, true, kActSoftmax, moments, max_nt);
     if (g.lds_fwd > kMaxLds) return ACE_EUNSUPPORTED;
+    // one launch, one block size: every level's geometry must use it
+    if (g.nt != L.nt) return ACE_EUNSUPPORTED;
     if (nblk + g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
     L.lv[l] = fwd_params(v.x, x_dtype, v.target, true, v.voxels, batch, channels, num_bins,
                          kActSoftmax, ignore_empty_classes, reduction, empty_weight, moments,

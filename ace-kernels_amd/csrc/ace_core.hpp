@@ -2187,6 +2187,8 @@ hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) 
       kern = prm.off ? fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, true>
                      : fwd_kernel_fast<T, CMAX, VEC, SOFT, RIGHT, false>;
       nt = g.nt;
+      // never more threads per block than the kernel was compiled for
+      if (nt > fast_bound<CMAX, SOFT>()) return hipErrorInvalidConfiguration;
     }
   }
   if (g.lds_fwd > 64 * 1024) {
@@ -2226,6 +2228,7 @@ hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) 
 // has the same configuration, so one instantiation serves all of them.
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_fwd_levels_t(long long nblk, size_t lds, const FwdLevels& L, hipStream_t s) {
+  if (L.nt > fast_bound<C, SOFT>()) return hipErrorInvalidConfiguration;
   auto kern = L.lv[0].off ? fwd_kernel_fast_levels<T, C, VEC, SOFT, RIGHT, true>
                           : fwd_kernel_fast_levels<T, C, VEC, SOFT, RIGHT, false>;
   if (lds > 64 * 1024) {
