@@ -1,4 +1,6 @@
-"""The reference-side ctypes binding printed in INTEGRATION.md section 3.
+"""The reference-side ctypes binding that the repository's integration notes
+print in their section 3 (the first python block there, read from the file
+named by ``DOC``).
 
 The block is executed as written, with the reference helpers it imports
 replaced by restatements of their layouts (the reference package itself is
@@ -43,7 +45,7 @@ def _binding_source() -> str:
     text = DOC.read_text()
     section = text.split("## 3.", 1)[1].split("\n## 4.", 1)[0]
     blocks = re.findall(r"```python\n(.*?)```", section, flags=re.S)
-    assert blocks, "INTEGRATION.md section 3 has no python block"
+    assert blocks, f"{DOC.name} section 3 has no python block"
     return blocks[0]
 
 
@@ -100,7 +102,7 @@ def load_binding(monkeypatch) -> dict:
         monkeypatch.setitem(sys.modules, name, mod)
     monkeypatch.setenv("ACE_HIP_LIB", str(_lib.LIB_PATH))
     ns: dict = {"__name__": "reference_binding"}
-    exec(compile(_binding_source(), "INTEGRATION.md#3", "exec"), ns)
+    exec(compile(_binding_source(), f"{DOC.name}#3", "exec"), ns)
     ns["__registered__"] = registered
     return ns
 
