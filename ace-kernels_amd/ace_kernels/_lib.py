@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # enums of include/ace_hip.h
 F32, BF16, F16, F64 = 0, 1, 2, 3
@@ -32,6 +32,7 @@ EXPORTS = (
     "ace_forward",
     "ace_backward",
     "ace_set_launch_events",
+    "ace_set_test_hooks",
     "ace_workspace_bytes_levels",
     "ace_forward_levels",
     "ace_backward_levels",
@@ -159,6 +160,8 @@ def lib() -> ctypes.CDLL:
     ]
     handle.ace_set_launch_events.restype = _i
     handle.ace_set_launch_events.argtypes = [_p, _p]
+    handle.ace_set_test_hooks.restype = _i
+    handle.ace_set_test_hooks.argtypes = [_i, _i]
     version = handle.ace_abi_version()
     if version != ABI_VERSION:
         raise AceLibraryError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}: rebuild it")

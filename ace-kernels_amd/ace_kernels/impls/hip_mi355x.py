@@ -135,26 +135,26 @@ def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False, shared: bool =
     dims = (pl.B, pl.C, pl.N, pl.K, binning, pl.dtype_code, int(pl.include_bg), pl.target_kind)
     ws = workspace(dev, stream, _workspace_bytes(dims))
     f64 = pl.dtype_code == _lib.F64
-    f32 = torch.float64 if f64 else torch.float32  # the outputs' type
+    out_dtype = torch.float64 if f64 else torch.float32  # the outputs' type
     # coef, d and jac (all saved for backward) share one allocation; the
     # per-class errors and the loss, which the caller may receive and modify
     # in place, have their own
     bck, bc = pl.B * pl.CL * pl.K, pl.B * pl.CL
     if shared:
-        saved = torch.empty(2 * bck + bc, dtype=f32, device=dev)
+        saved = torch.empty(2 * bck + bc, dtype=out_dtype, device=dev)
         coef = saved[:bck].view(pl.B, pl.CL, pl.K)
         d = saved[bck:2 * bck].view(pl.B, pl.CL, pl.K)
         jac = saved[2 * bck:].view(pl.B, pl.CL)
     else:
-        coef = torch.empty((pl.B, pl.CL, pl.K), dtype=f32, device=dev)
+        coef = torch.empty((pl.B, pl.CL, pl.K), dtype=out_dtype, device=dev)
         d = torch.empty_like(coef)
-        jac = torch.empty((pl.B, pl.CL), dtype=f32, device=dev)
-    per_class = torch.empty((pl.B, pl.CL), dtype=f32, device=dev)
+        jac = torch.empty((pl.B, pl.CL), dtype=out_dtype, device=dev)
+    per_class = torch.empty((pl.B, pl.CL), dtype=out_dtype, device=dev)
     reduction = _REDUCTIONS[config.reduction]
-    loss = torch.empty((), dtype=f32, device=dev) if reduction != _lib.RED_NONE else None
+    loss = torch.empty((), dtype=out_dtype, device=dev) if reduction != _lib.RED_NONE else None
     st = torch.empty((3, pl.B, pl.CL, pl.K), dtype=torch.float64, device=dev) if stats else None
     weights = class_weights(config, pl.CL)
-    cw = class_weight_tensor(tuple(weights), dev, f32) if weights is not None else None
+    cw = class_weight_tensor(tuple(weights), dev, out_dtype) if weights is not None else None
     if f64:
         rc = lib.ace_forward_f64(
             pl.x.data_ptr(), pl.target.data_ptr(), pl.target_kind,

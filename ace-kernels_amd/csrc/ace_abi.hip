@@ -10,6 +10,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "ace_core.hpp"
@@ -69,22 +70,6 @@ namespace {
 
 constexpr size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
 
-// Tuning knob for experiments: vector steps per block (0 = automatic).
-int env_steps(const char* name) {
-  const char* v = getenv(name);
-  if (!v) return 0;
-  const int s = atoi(v);
-  return s > 0 && s <= 1024 ? s : 0;
-}
-
-// Tuning knob for experiments: histogram copies per block (power of two <= 64).
-int env_copies() {
-  const char* v = getenv("ACE_FWD_COPIES");
-  if (!v) return 0;
-  const int c = atoi(v);
-  return (c == 1 || c == 2 || c == 4 || c == 8 || c == 16 || c == 32 || c == 64) ? c : 0;
-}
-
 size_t elem_size(int dtype) { return dtype == ACE_F32 ? 4 : 2; }
 
 // Bytes of the targets: int64 class labels [B, N] or float32 one-hot [B, C, N].
@@ -137,8 +122,7 @@ bool use_moments(bool soft, bool labels, int act, int64_t batch, int64_t channel
         num_bins <= kMomentMaxBins))
     return false;
   const Geometry g = make_geometry(batch, channels, voxels, num_bins, true, include_background != 0,
-                                   true, env_steps("ACE_FWD_STEPS"), env_copies(), true, true,
-                                   kThreads);
+                                   true, 0, 0, true, true, kThreads);
   return g.lds_fwd <= kMaxLds && g.lds_bwd <= kMaxLds;
 }
 
@@ -149,41 +133,21 @@ bool fast_forward(bool soft, bool labels, int act, int64_t channels, bool moment
   return act == kActSoftmax && labels && fast_channels(channels) && (!soft || moments);
 }
 
-// Bound of the loss block's wait for another batch epilogue's partial word:
-// kMaxPolls, or ACE_FWD_MAX_POLLS (a test knob: 0 makes the wait give up at
-// once wherever the word has not arrived, the loss NaN, with every kernel
-// still exiting normally).
-int env_max_polls() {
-  const char* v = getenv("ACE_FWD_MAX_POLLS");
-  if (!v) return kMaxPolls;
-  const int n = atoi(v);
-  return n >= 0 && n <= kMaxPolls ? n : kMaxPolls;
-}
-
-// Test knob: ACE_FWD_PUBLISH_DELAY sleeps (s_sleep 2 each, at most 2^16)
-// before a batch epilogue publishes its loss partial word, so that a test
-// can make the loss block's bounded wait give up (0 otherwise).
-int env_publish_delay() {
-  const char* v = getenv("ACE_FWD_PUBLISH_DELAY");
-  if (!v) return 0;
-  const int n = atoi(v);
-  return n >= 0 && n <= (1 << 16) ? n : 0;
-}
-
-// Tuning knob for experiments: largest forward block size (256 or 1024).
-int env_max_threads() {
-  const char* v = getenv("ACE_FWD_MAX_THREADS");
-  return (v && atoi(v) == kThreads) ? kThreads : kFastThreads;
-}
+// Test hooks (ace_set_test_hooks), process-wide: the bound of the loss
+// block's wait for another batch epilogue's partial word (kMaxPolls; 0 makes
+// the wait give up at once wherever the word has not arrived, the loss NaN,
+// with every kernel still exiting normally), and sleeps (s_sleep 2 each)
+// before a batch epilogue publishes its word (0), so that a test can make
+// that wait give up.
+std::atomic<int> g_max_polls{kMaxPolls};
+std::atomic<int> g_publish_delay{0};
 
 // Forward geometry of one problem (the kernel the launcher will pick).
 Geometry forward_geometry(int64_t batch, int64_t channels, int64_t voxels, int num_bins, bool soft,
                           int include_background, bool labels, int act, bool moments,
                           int max_nt = kFastThreads) {
-  const int cap = env_max_threads();
-  return make_geometry(batch, channels, voxels, num_bins, soft, include_background != 0, labels,
-                       env_steps("ACE_FWD_STEPS"), env_copies(), moments,
-                       fast_forward(soft, labels, act, channels, moments), max_nt < cap ? max_nt : cap);
+  return make_geometry(batch, channels, voxels, num_bins, soft, include_background != 0, labels, 0, 0,
+                       moments, fast_forward(soft, labels, act, channels, moments), max_nt);
 }
 
 // The activation is not an argument here: the largest workspace of the
@@ -205,8 +169,7 @@ size_t workspace_size(int64_t batch, int64_t channels, int64_t voxels, int num_b
   return best;
 }
 
-// Vector steps per backward block: ACE_BWD_STEPS, else make_geometry's
-// choice (~1024 blocks; 512 above 8 channels, where the forward's final-sum
+// Vector steps per backward block: make_geometry's choice (~1024 blocks; 512 above 8 channels, where the forward's final-sum
 // atomics set the count) -- except the fast 16-channel backward with every
 // channel in the loss, which holds 4 or more waves per SIMD (ace_core.hpp:
 // bwd_min_waves) and measured fastest with ~1024 blocks on MI355X (cfg 4,
@@ -214,13 +177,33 @@ size_t workspace_size(int64_t batch, int64_t channels, int64_t voxels, int num_b
 // two voxels per lane: 50.8 against 57.2 at 512).
 int bwd_steps(bool soft, bool labels, int act, int64_t batch, int64_t channels, int64_t voxels,
               int include_background, bool moments) {
-  const int env = env_steps("ACE_BWD_STEPS");
-  if (env > 0) return env;
   const bool fast = act == kActSoftmax && fast_channels(channels) && (!soft || (labels && moments));
   if (!(fast && channels > 8 && (include_background != 0 || channels == 1))) return 0;
   const int64_t step_vox = (int64_t)kThreads * variant_for(channels).vec;
   const int64_t steps = cdiv(batch * (voxels > 0 ? voxels : 1), step_vox * 1024);
   return (int)(steps < 1 ? 1 : (steps > 64 ? 64 : steps));
+}
+
+// The forward's launch plan and the checks it must pass before anything is
+// launched: the geometry of the kernel the launcher will pick, within the
+// LDS and the grid's limits.
+struct ForwardPlan {
+  int rc;
+  int act;
+  bool moments;
+  Geometry g;
+};
+ForwardPlan plan_forward(int64_t batch, int64_t channels, int64_t voxels, int num_bins, int binning,
+                         int activation, int include_background, int target_kind) {
+  ForwardPlan fp{};
+  const bool soft = binning == ACE_SOFT;
+  const bool labels = target_kind == ACE_TARGET_LABELS_I64;
+  fp.act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
+  fp.moments = use_moments(soft, labels, fp.act, batch, channels, voxels, num_bins, include_background);
+  fp.g = forward_geometry(batch, channels, voxels, num_bins, soft, include_background, labels, fp.act,
+                          fp.moments);
+  fp.rc = (fp.g.lds_fwd > kMaxLds || fp.g.nblk > 0x7fffffffLL) ? ACE_EUNSUPPORTED : ACE_OK;
+  return fp;
 }
 
 // fast_bin's fixed point and edge margin for K bins (ace_bins.hpp:
@@ -268,9 +251,12 @@ FwdParams fwd_params(const void* x, int x_dtype, const void* target, bool labels
   p.red = reduction;
   p.empty_w = empty_weight;
   p.packed = g.packed ? 1 : 0;
-  p.max_polls = env_max_polls();
-  p.publish_delay = env_publish_delay();
+  p.max_polls = g_max_polls.load(std::memory_order_relaxed);
+  p.publish_delay = g_publish_delay.load(std::memory_order_relaxed);
   p.pscale = 1.0 / 1073741824.0;  // the generic kernels' sums: 30-bit fixed point
+  const int sf = soft_frac(voxels);  // the generic soft sums: finer (soft_frac)
+  p.sfx = ldexpf(1.0f, sf);
+  p.sscale = ldexp(1.0, -sf);
   if (g.fast && !moments) set_fast_bins(p, num_bins, channels);
   if (moments) {
     const MomentScale ms = moment_scale(num_bins);
@@ -423,7 +409,7 @@ using namespace ace;
 
 extern "C" {
 
-int ace_abi_version(void) { return 6; }
+int ace_abi_version(void) { return 7; }
 
 const char* ace_error_string(int code) {
   switch (code) {
@@ -472,14 +458,13 @@ int ace_forward(const void* x, int x_dtype, const void* target, int target_kind,
   if (reduction != ACE_RED_NONE && !loss) return ACE_EINVAL;
   const bool soft = binning == ACE_SOFT;
   const bool labels = target_kind == ACE_TARGET_LABELS_I64;
-  const int act = (activation == ACE_ACT_SOFTMAX && channels == 1) ? kActNone : activation;
-  const bool moments =
-      use_moments(soft, labels, act, batch, channels, voxels, num_bins, include_background);
-  const Geometry g = forward_geometry(batch, channels, voxels, num_bins, soft, include_background,
-                                      labels, act, moments);
+  const ForwardPlan fp = plan_forward(batch, channels, voxels, num_bins, binning, activation,
+                                      include_background, target_kind);
+  if (fp.rc) return fp.rc;
+  const Geometry& g = fp.g;
+  const int act = fp.act;
+  const bool moments = fp.moments;
   if (workspace_bytes < g.ws_bytes) return ACE_EWORKSPACE;
-  if (g.lds_fwd > kMaxLds) return ACE_EUNSUPPORTED;
-  if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
 
   const FwdParams p = fwd_params(x, x_dtype, target, labels, voxels, batch, channels, num_bins, act,
                                   ignore_empty_classes, reduction, empty_weight, moments, class_weight,
@@ -649,8 +634,9 @@ int ace_forward_noalloc(const void* x, int x_dtype, const void* target, int targ
                         const float* class_weight, const float* bin_table,
                         const float* centre_table, float* coef, float* diff, float* jac,
                         float* per_class, float* loss, double* stats, void* stream) {
-  // the checks ace_forward makes before it looks at the workspace, so that an
-  // invalid call launches nothing
+  // the checks ace_forward makes before it looks at the workspace (arguments,
+  // then the launch plan), so that an invalid or unsupported call launches
+  // nothing
   int rc = check_common(x, x_dtype, target, target_kind, batch, channels, voxels, num_bins,
                         binning, activation, bin_table, centre_table, true);
   if (rc) return rc;
@@ -658,6 +644,9 @@ int ace_forward_noalloc(const void* x, int x_dtype, const void* target, int targ
     return ACE_EINVAL;
   if (!coef || !diff || !jac || !per_class) return ACE_EINVAL;
   if (reduction != ACE_RED_NONE && !loss) return ACE_EINVAL;
+  rc = plan_forward(batch, channels, voxels, num_bins, binning, activation, include_background,
+                    target_kind).rc;
+  if (rc) return rc;
   const size_t need = ace_workspace_reset_bytes(batch, channels, voxels, num_bins, binning, x_dtype,
                                                 include_background, target_kind);
   if (need == 0) return ACE_EINVAL;
@@ -682,6 +671,13 @@ int ace_forward_noalloc(const void* x, int x_dtype, const void* target, int targ
 
 int ace_set_launch_events(void* start, void* stop) {
   launch_events() = LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
+  return ACE_OK;
+}
+
+int ace_set_test_hooks(int max_polls, int publish_delay) {
+  if (max_polls > kMaxPolls || publish_delay > (1 << 16)) return ACE_EINVAL;
+  g_max_polls.store(max_polls < 0 ? kMaxPolls : max_polls, std::memory_order_relaxed);
+  g_publish_delay.store(publish_delay < 0 ? 0 : publish_delay, std::memory_order_relaxed);
   return ACE_OK;
 }
 

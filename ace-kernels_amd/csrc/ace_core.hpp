@@ -73,6 +73,8 @@ struct FwdParams {
   uint32_t qmask;      // 2^qs - 1
   int qs;
   double pscale;       // value of one unit of the hard sums of p (fast: 1 / (K 2^qs), else 2^-30)
+  float sfx;           // generic soft sums: fixed-point scale 2^f (soft_frac)
+  double sscale;       // 2^-f
   float msc;           // soft moments: 2^m, the fixed-point scale of p (moment_scale)
   float misc;          // 2^-m
   int mw;              // soft moments: half-bin h has base h mw (in units of 2^-m)
@@ -358,6 +360,12 @@ __device__ __forceinline__ SoftW soft_assign(float p, int K, float n2f, const fl
 __device__ __forceinline__ long long fx(float v) {
   return (long long)(int)rintf(v * 1073741824.0f);
 }
+// The same at scale sfx = 2^f (soft_frac: up to 2^40), exact for
+// |v| >= 2^(23 - f): v sfx is exact in float32 and below 2^41, so it is
+// converted through float64.
+__device__ __forceinline__ long long fx_soft(float v, float sfx) {
+  return (long long)__builtin_rint((double)(v * sfx));
+}
 
 __device__ __forceinline__ void lds_add(unsigned long long* p, unsigned long long v) {
   __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -553,10 +561,10 @@ __device__ __forceinline__ void fwd_accumulate(const FwdParams& P, const Hist& H
         const SoftW w = soft_assign<RIGHT>(p[c], K, nf, btab, repl);
         const int sl = ((c - off) * K + w.l) * R + copy;
         const int sr = ((c - off) * K + w.r) * R + copy;
-        lds_add(&H.w[sl], fx(w.lw));
-        lds_add(&H.w[sr], fx(w.rw));
-        lds_add(&H.p[sl], fx(w.lw * p[c]));
-        lds_add(&H.p[sr], fx(w.rw * p[c]));
+        lds_add(&H.w[sl], fx_soft(w.lw, P.sfx));
+        lds_add(&H.w[sr], fx_soft(w.rw, P.sfx));
+        lds_add(&H.p[sl], fx_soft(w.lw * p[c], P.sfx));
+        lds_add(&H.p[sr], fx_soft(w.rw * p[c], P.sfx));
         if (labels) {
           const bool hit = lab[j] == c;
           gl = hit ? sl : gl;
@@ -566,14 +574,14 @@ __device__ __forceinline__ void fwd_accumulate(const FwdParams& P, const Hist& H
         } else {
           const float y = yv[c][j];
           if (y != 0.0f) {
-            lds_add(&H.g[sl], fx(w.lw * y));
-            lds_add(&H.g[sr], fx(w.rw * y));
+            lds_add(&H.g[sl], fx_soft(w.lw * y, P.sfx));
+            lds_add(&H.g[sr], fx_soft(w.rw * y, P.sfx));
           }
         }
       }
       if (labels && lab[j] >= off) {
-        lds_add(&H.g[gl], fx(glw));
-        lds_add(&H.g[gr], fx(grw));
+        lds_add(&H.g[gl], fx_soft(glw, P.sfx));
+        lds_add(&H.g[gr], fx_soft(grw, P.sfx));
       }
     }
   }
@@ -773,9 +781,11 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
       Pd = (double)sm[1] * pscale;
     } else {
       zero_sums<3>(fb_of(i), NV, reps, CK, t);
-      Wd = (double)sm[0] * dscale;
-      Pd = (double)sm[1] * pscale;
-      Gd = (double)sm[2] * dscale;
+      // generic soft sums at 2^f (soft_frac), hard ones at 2^30
+      const double ws = SOFT ? P.sscale : dscale;
+      Wd = (double)sm[0] * ws;
+      Pd = (double)sm[1] * (SOFT ? P.sscale : pscale);
+      Gd = (double)sm[2] * ws;
     }
     const int64_t o = (int64_t)(b0 + bb) * CK + t;
     if (P.stats) {
@@ -787,7 +797,16 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
     const float Pf = (float)Pd;
     const float Gf = (float)Gd;
     const bool empty = SOFT ? !(Wf >= P.empty_w) : (Wf == 0.0f);
-    const float dd = empty ? 0.0f : (Pf / Wf - Gf / Wf);
+    // d = P/W - G/W in the reference's float32 order (binning.py:136-141):
+    // two quotients rounded to float32, then their difference.  Soft binning
+    // forms the quotients from the float64 sums (one rounding each instead of
+    // rounding the sums first): the soft gradient takes d amplified by
+    // 2K / W through (p - y - d) / S, and in a bin of one voxel the moments'
+    // quotients are then exactly (the quantised) p and y, so d = fl(p - y)
+    // cancels the backward's float32 residual fl(p - y), as in the reference.
+    float dd = 0.0f;
+    if (!empty)
+      dd = SOFT ? (float)(Pd / Wd) - (float)(Gd / Wd) : Pf / Wf - Gf / Wf;
     sd[i] = dd;
     sw[i] = Wf;
     sg[i] = Gf;
@@ -1882,12 +1901,20 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
 // moments forward (lw = (cr - p) / S, rw = (p - cl) / S, S = cr - cl), the
 // soft dL/dp of v2_autograd.py:94-104,
 //   g (coef_l (lw - (p - y - d_l) / S) + coef_r (rw + (p - y - d_r) / S)),
-// is linear in p and y: g/S (coef_l (cr + d_l) - coef_r (cl + d_r))
-// + 2 g/S (coef_r - coef_l) (p - y/2).  sab[2h], sab[2h + 1] hold the two
-// coefficients (computed in float64) for half-bin h of every loss channel.
-__device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const float* repl,
-                                                           const float* scoef, const float* sdd,
-                                                           const float* sg, int K, int CL) {
+// is linear in p and y: A + B (p - y/2) with A = g/S (coef_l (cr + d_l) -
+// coef_r (cl + d_r)) and B = 2 g/S (coef_r - coef_l).  A and B are each of
+// the order of 2K coef g, while dL/dp is a small residual wherever p - y - d
+// is small (bins of a few well-calibrated voxels), so the form is evaluated
+// from the half-bin's lower boundary e instead: A_y + B (p - e) with
+// A_y = A + B (e - y/2) formed in float64 for y = 0 and y = 1.  p - e is
+// exact in float32 (e <= p <= 2e for h >= 1, Sterbenz; e = 0 for h = 0) and
+// at most 1/(2K), so no float32 term is larger than dL/dp by more than ~2
+// coef g.  sab[4h .. 4h + 3] = (A_0, A_1, B, e) for half-bin h of every loss
+// channel; tab is the padded half-boundary table (tab[h] = e for h >= 1).
+__device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const float* tab,
+                                                           const float* repl, const float* scoef,
+                                                           const float* sdd, const float* sg,
+                                                           int K, int CL) {
   const int H = 2 * K;
   for (int t = threadIdx.x; t < CL * H; t += kThreads) {
     const int cl = t / H;
@@ -1897,8 +1924,12 @@ __device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const flo
     const double cL = repl[hh], cR = repl[hh + 2];
     const double gs = (double)sg[cl] / (cR - cL);
     const double kl = scoef[cl * K + l], kr = scoef[cl * K + r];
-    sab[2 * t] = (float)(gs * (kl * (cR + (double)sdd[cl * K + l]) - kr * (cL + (double)sdd[cl * K + r])));
-    sab[2 * t + 1] = (float)(2.0 * gs * (kr - kl));
+    const double A = gs * (kl * (cR + (double)sdd[cl * K + l]) - kr * (cL + (double)sdd[cl * K + r]));
+    const double Bc = 2.0 * gs * (kr - kl);
+    const float e = hh == 0 ? 0.0f : tab[hh];
+    const float4 v = make_float4((float)(A + Bc * (double)e), (float)(A + Bc * ((double)e - 0.5)),
+                                 (float)Bc, e);
+    *reinterpret_cast<float4*>(sab + 4 * t) = v;
   }
 }
 
@@ -1917,7 +1948,16 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
     softmax_fast<C>(p);
     float gp[C];
     uint32_t lab = 0xffffffffu;
-    if constexpr (SOFT) lab = fast_label<C>(t.lab[j]);
+    // soft: half the rounding error of the labelled channel's float32
+    // residual p - 1 (see below), once per voxel
+    float hrho = 0.0f;
+    if constexpr (SOFT) {
+      lab = fast_label<C>(t.lab[j]);
+      float pl = p[0];
+#pragma unroll
+      for (int c = 1; c < C; ++c) pl = lab == (uint32_t)c ? p[c] : pl;
+      hrho = 0.5f * (((pl - 1.0f) + 1.0f) - pl);
+    }
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       gp[c] = 0.0f;
@@ -1928,9 +1968,16 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
         gp[c] = scoef[cl * K + k] * sg[cl];
       } else {
         const int h = bucket_unit<RIGHT>(p[c], nf, tab);
-        const float2 ab = *reinterpret_cast<const float2*>(sab + 2 * (cl * 2 * K + h));
-        const float y = lab == (uint32_t)c ? 0.5f : 0.0f;
-        gp[c] = fmaf(ab.y, p[c] - y, ab.x);
+        const float4 ab = *reinterpret_cast<const float4*>(sab + 4 * (cl * 2 * K + h));
+        const bool hit = lab == (uint32_t)c;
+        // the reference's residual is the float32 p - y (v2_autograd.py:
+        // 94-104); for y = 1 it is p - 1 + rho with rho = (fl(p - 1) + 1) - p,
+        // exact (fl(p - 1) + 1 and p are within a factor two, or the former
+        // is 0), and the linear form, exact in p - y, adds B/2 rho: t = p - e
+        // (exact) plus rho/2, rounded once (an error below 2^-24 t).  In a bin
+        // of one voxel d = fl(p - y) then cancels the residual exactly.
+        const float tt = (p[c] - ab.w) + (hit ? hrho : 0.0f);
+        gp[c] = fmaf(ab.z, tt, hit ? ab.y : ab.x);
       }
     }
     float dot = 0.0f;
@@ -1958,8 +2005,9 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
   float* scoef = tabs + tab_floats;
   float* sdd = scoef + CK;
   float* sg = sdd + (SOFT ? CK : 0);
-  // soft: (A, B) per half-bin, 8-byte aligned after g
-  float* sab = sg + ((CL + 1) & ~1);
+  // soft: (A_0, A_1, B, e) per half-bin, 16-byte aligned after g (tab_floats
+  // is a multiple of 4; the host sizes the region the same way)
+  float* sab = tabs + (((size_t)tab_floats + (size_t)CK * (SOFT ? 2 : 1) + CL + 3) & ~(size_t)3);
   const int nrepl = SOFT ? 2 * K + 2 : 0;
 
   const int64_t N = P.N;
@@ -2019,7 +2067,7 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
   const float* tab = tabs;
   const float* repl = tabs + n + 2;
   if constexpr (SOFT) {
-    soft_half_bin_coefficients(sab, repl, scoef, sdd, sg, K, CL);
+    soft_half_bin_coefficients(sab, tab, repl, scoef, sdd, sg, K, CL);
     __syncthreads();
   }
 
@@ -2063,12 +2111,11 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
 }
 
 // One problem per launch: block blockIdx.x of P's grid.
-// Block size bound: kFastThreads for hard binning with C <= 4; kThreads
-// otherwise (16 channels of two tiles in flight need more than the 128 VGPRs
-// of 16 waves per CU; soft moments run in 256-thread blocks, make_geometry).
+// Block size bound of the fast forward kernels (ace_geometry.hpp:
+// fast_fwd_bound).
 template <int C, bool SOFT>
 constexpr int fast_bound() {
-  return (C <= 4 && !SOFT) ? kFastThreads : kThreads;
+  return fast_fwd_bound(C, SOFT);
 }
 // Backward: at least 4 waves per SIMD (at most 128 VGPRs) for the
 // 16-channel kernel with every channel in the loss, whose grid is sized for

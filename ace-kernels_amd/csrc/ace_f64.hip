@@ -36,6 +36,10 @@ namespace ace {
 namespace f64 {
 
 constexpr size_t kMaxLds64 = 160 * 1024;
+// Static LDS of fwd64_kernel (s_rows: 64 doubles, s_last: one int, 16-byte
+// aligned); its dynamic LDS must fit beside it.
+constexpr size_t kFwdStaticLds64 = 64 * sizeof(double) + 16;
+constexpr size_t kMaxFwdDynLds64 = kMaxLds64 - kFwdStaticLds64;
 constexpr int kMaxTiles64 = 256;  // blocks per batch index: the last block reads them all
 
 struct Geo64 {
@@ -65,7 +69,7 @@ inline Geo64 geometry(int64_t B, int64_t C, int64_t N, int K, bool soft, bool in
   g.tab_bytes = align_up((size_t)g.ntab * sizeof(double), 16);
   g.waves = 0;
   for (int w : {4, 2, 1}) {
-    if (g.tab_bytes + (size_t)w * g.nv * sizeof(double) <= kMaxLds64) {
+    if (g.tab_bytes + (size_t)w * g.nv * sizeof(double) <= kMaxFwdDynLds64) {
       g.waves = w;
       break;
     }
@@ -548,13 +552,15 @@ int ace_forward_f64(const double* x, const void* target, int target_kind, int64_
   // the epilogue reuses the histogram LDS: 3 C'K sums, C'K d, C'K empty flags
   const size_t epi = g.tab_bytes + (size_t)4 * g.ck * 8 + align_up((size_t)g.ck, 16);
   const size_t lds = g.lds > epi ? g.lds : epi;
+  // refused before any HIP call: the dynamic LDS beside the kernel's static
+  // arrays must fit the workgroup's
+  if (lds > kMaxFwdDynLds64) return ACE_EUNSUPPORTED;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(
         reinterpret_cast<const void*>(soft ? fwd64_kernel<true> : fwd64_kernel<false>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return code_of(e);
   }
-  if (lds > kMaxLds64) return ACE_EUNSUPPORTED;
   return code_of(soft ? launch(fwd64_kernel<true>, nblk, lds, s, p, nt)
                       : launch(fwd64_kernel<false>, nblk, lds, s, p, nt));
 }

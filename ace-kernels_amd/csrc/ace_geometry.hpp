@@ -100,8 +100,30 @@ inline bool stream_problem(size_t x_bytes, size_t target_bytes) {
   return 2 * x_bytes + target_bytes > kStreamBytes;
 }
 
+// Fraction bits of the generic soft kernels' fixed-point sums of weights,
+// weight * p and weight * y (each term below 2): 40, or fewer for a batch
+// index of more than 2^19 voxels, so that a bin's sum (at most N terms that
+// add to at most N) stays below 2^61.  With 30 bits a small weight times p
+// lost bits (exact only from 2^-7), and the soft gradient amplifies d's
+// error by 2K / W in bins of a few voxels; with 40 the terms are exact from
+// 2^-17.
+inline int soft_frac(int64_t voxels) {
+  int bits = 0;
+  while (bits < 62 && (1ll << bits) <= voxels) ++bits;  // bit length of N
+  const int f = 60 - bits;
+  return f < 40 ? (f < 1 ? 1 : f) : 40;
+}
+
 // Channel counts served by the fast (softmax + class-index labels) kernels.
 inline bool fast_channels(int64_t C) { return C == 2 || C == 3 || C == 4 || C == 16; }
+
+// Launch bound of the fast forward kernel for C channels (its compile-time
+// channel variant): kFastThreads for hard binning with C <= 4, kThreads
+// otherwise (16 channels with two tiles in flight need more than the 128
+// VGPRs of 16 waves per CU; soft moments run in 256-thread blocks).  The
+// launchers refuse a block size above it, and make_geometry never picks one
+// (tests/test_geometry.py checks every configuration the fast kernels serve).
+constexpr int fast_fwd_bound(int C, bool soft) { return (C <= 4 && !soft) ? kFastThreads : kThreads; }
 
 struct Geometry {
   Variant var;
@@ -240,10 +262,10 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   const size_t epi = epi_layout(g.ck, g.CL, 1, moments).bytes;
   const size_t region = hist > epi ? hist : epi;
   g.lds_fwd = g.tab_floats * 4 + region;
-  // backward: tables + coef (+ d) + g (+ two coefficients per half-bin for
-  // soft moments)
-  g.lds_bwd = g.tab_floats * 4 +
-              align_up((size_t)g.ck * (soft ? 2 : 1) + ((g.CL + 1) & ~1) + (moments ? 4 * g.ck : 0), 4) * 4;
+  // backward: tables + coef (+ d) + g, then for soft moments four values per
+  // half-bin from a 16-byte boundary (bwd_fast_body)
+  g.lds_bwd = (align_up(g.tab_floats + (size_t)g.ck * (soft ? 2 : 1) + (size_t)g.CL, 4) +
+               (moments ? 8 * (size_t)g.ck : 0)) * 4;
   // workspace: ticket counters (groups, batch indices, loss), one loss
   // partial word per batch index and the final sums; it must start zero and
   // every call leaves it zero

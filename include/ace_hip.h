@@ -251,6 +251,19 @@ int ace_forward_noalloc(const void* x, int x_dtype, const void* target,
  */
 int ace_set_launch_events(void* start, void* stop);
 
+/*
+ * Test hooks.  No counterpart in the reference: they let a test force the
+ * forward's cross-block failure handling from the host, with every kernel
+ * still exiting normally.  Process-wide, read by each later forward call.
+ * max_polls bounds the loss block's wait for another batch index's partial
+ * loss word (default 2^20 polls; 0 gives up at once wherever the word has
+ * not arrived, and that loss is then NaN); publish_delay makes each batch
+ * epilogue sleep about 128 * publish_delay cycles (s_sleep 2 each) before it publishes its
+ * word (default 0).  A negative value restores the default.  Returns
+ * ACE_EINVAL for max_polls > 2^20 or publish_delay > 2^16, else ACE_OK.
+ */
+int ace_set_test_hooks(int max_polls, int publish_delay);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,19 @@ def run(impl: str, x: torch.Tensor, y: torch.Tensor, config: ACEConfig, upstream
     return loss.detach(), grad
 
 
+def truth64(x: torch.Tensor, y: torch.Tensor, config: ACEConfig, upstream=None):
+    """(loss, grad) in float64 throughout: the oracle's v2 path (the
+    handwritten gradient of ``impls/v2_autograd.py``) on float64 logits on
+    the CPU.  The reference loss itself is no float64 result on float64
+    logits: it casts the probabilities to float32 before binning
+    (``hardl1ace.py:84-85``, ``softl1ace.py:84-85``), so its sums and its
+    autograd backward run in float32."""
+    from oracle.v2 import register_v2
+
+    register_v2()
+    return run("v2_recompute", x.detach().cpu().double(), y.detach().cpu(), config, upstream)
+
+
 def hip_stats(x: torch.Tensor, y: torch.Tensor, config: ACEConfig):
     """(loss, coef, d, jac, per_class, stats[3,B,C',K] float64) of one forward."""
     pl = hip.make_plan(x, y, config)

@@ -138,6 +138,50 @@ def test_noalloc_source_calls_no_allocator() -> None:
     assert "hipGetSymbolAddress" in body and "HIP_SYMBOL(scratch)" in body
 
 
+def test_no_environment_knobs() -> None:
+    """The library reads no environment variable: the launch geometry and
+    the loss block's wait depend on the call's arguments alone.  The forward's
+    give-up path is reached through ace_set_test_hooks, which checks its
+    arguments and restores the defaults for negative values."""
+    csrc = Path(__file__).resolve().parents[1] / "ace-kernels_amd" / "csrc"
+    for src in sorted(csrc.glob("*.hip")) + sorted(csrc.glob("*.hpp")):
+        assert "getenv" not in src.read_text(), src.name
+    lib = _lib.lib()
+    assert lib.ace_set_test_hooks((1 << 20) + 1, 0) == 1
+    assert lib.ace_set_test_hooks(0, (1 << 16) + 1) == 1
+    assert lib.ace_set_test_hooks(0, 2000) == 0
+    assert lib.ace_set_test_hooks(-1, -1) == 0
+
+
+def test_f64_forward_refuses_lds_beside_its_static_arrays() -> None:
+    """ace_forward_f64 refuses, before any HIP call, a layout whose dynamic
+    LDS fits the 160 KiB workgroup alone but not beside the kernel's static
+    arrays (64 doubles and an int, 528 bytes).  Its dynamic LDS at hard
+    binning with C' = 2 is the larger of the wave histograms and the
+    epilogue's layout (tables, 4 C'K doubles, C'K flag bytes), so K near 2210
+    lands in that band.  Only refused configurations are called here (fake
+    pointers)."""
+    lib = _lib.lib()
+    fake = 256
+    limit, static = 160 * 1024, 64 * 8 + 16
+
+    def dyn_lds(k):
+        ck = 2 * k
+        tab = (k * 8 + 15) // 16 * 16
+        nv = 3 * ck
+        waves = next((w for w in (4, 2, 1) if tab + w * nv * 8 <= limit - static), 1)
+        epi = tab + 4 * ck * 8 + (ck + 15) // 16 * 16
+        return max(tab + waves * nv * 8, epi)
+
+    band = [k for k in range(1500, 3000) if limit - static < dyn_lds(k) <= limit]
+    assert band, "no bin count in the band"
+    for k in band + [k for k in range(1500, 3000) if dyn_lds(k) > limit][:3]:
+        args = [fake, fake, _lib.TARGET_LABELS_I64, 2, 2, 64, k, _lib.HARD, _lib.ACT_SOFTMAX,
+                1, 1, _lib.RED_MEAN, 0, 0.01, None, fake, None, fake, 1 << 40, fake, fake, fake, fake,
+                fake, None, None]
+        assert lib.ace_forward_f64(*args) == 2, k  # ACE_EUNSUPPORTED
+
+
 def test_f64_entry_points_validate_before_launch() -> None:
     """ace_forward_f64 / ace_backward_f64 reject bad arguments before any HIP
     call; ace_workspace_bytes sizes their workspace for x_dtype ACE_F64."""

@@ -29,7 +29,7 @@ from hypothesis import strategies as st
 
 from ace_kernels import ACEConfig
 from ace_kernels import measure as m
-from gpu_helpers import LOSS_ATOL, LOSS_RTOL, assert_grad_close, run, say
+from gpu_helpers import LOSS_ATOL, LOSS_RTOL, assert_grad_close, run, say, truth64
 
 pytestmark = pytest.mark.gpu
 
@@ -73,7 +73,7 @@ def test_hip_matches_reference(case) -> None:
     loss_ref, grad_ref = run("reference", x, y, cfg)
     torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
     if cfg.binning == "soft" and x[0, 0].numel() < 8 * cfg.num_bins:
-        _, grad64 = run("reference", x.double(), y, cfg)
+        _, grad64 = truth64(x, y, cfg)
         assert_grad_close(grad, grad_ref, x, cfg, rtol=1e-3, truth=grad64)
     else:
         assert_grad_close(grad, grad_ref, x, cfg)

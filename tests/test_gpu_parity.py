@@ -29,7 +29,8 @@ import pytest
 import torch
 
 from ace_kernels import ACEConfig
-from gpu_helpers import GRAD_ATOL, LOSS_ATOL, LOSS_RTOL, assert_grad_close, assert_lowp_grad_close, run, say
+from gpu_helpers import (GRAD_ATOL, LOSS_ATOL, LOSS_RTOL, assert_grad_close, assert_lowp_grad_close, run, say,
+                         truth64)
 
 pytestmark = pytest.mark.gpu
 
@@ -74,7 +75,7 @@ def test_matches_reference(binning, b, c, spatial, kw) -> None:
     torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
     voxels = x[0, 0].numel()
     if binning == "soft" and voxels < 8 * cfg.num_bins:
-        _, grad64 = run("reference", x.double(), y, cfg)
+        _, grad64 = truth64(x, y, cfg)
         assert_grad_close(grad, grad_ref, x, cfg, rtol=1e-3, truth=grad64)
     else:
         assert_grad_close(grad, grad_ref, x, cfg)
@@ -131,7 +132,7 @@ def test_many_bins(binning, c, k) -> None:
     loss_ref, grad_ref = _oracle(x, y, cfg)
     torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
     if binning == "soft":
-        _, grad64 = run("reference", x.double(), y, cfg)
+        _, grad64 = truth64(x, y, cfg)
         h = grad.cpu().double() - grad64
         r = grad_ref.double() - grad64
         assert float(h.norm()) <= 2.0 * float(r.norm()) + GRAD_ATOL * h.numel() ** 0.5, (h.norm(), r.norm())

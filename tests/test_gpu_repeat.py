@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from ace_kernels import ACEConfig
-from ace_kernels import common
+from ace_kernels import _lib, common
 from ace_kernels.impls import hip_mi355x as hip
 from gpu_helpers import say
 
@@ -55,11 +55,11 @@ def test_repeated_forwards_are_identical_and_leave_the_workspace_zero(binning, b
 
 
 @pytest.mark.parametrize("binning", ["hard", "soft"])
-def test_abandoned_loss_words_leave_the_workspace_zero(monkeypatch, binning) -> None:
+def test_abandoned_loss_words_leave_the_workspace_zero(binning) -> None:
     """The loss block's bounded wait for the other batch epilogues' partial
-    words, forced from the host to give up: ACE_FWD_MAX_POLLS=0 (no polls)
-    and ACE_FWD_PUBLISH_DELAY (the other epilogues sleep ~0.1 ms before they
-    publish), both read per call; every kernel still exits normally.  A loss
+    words, forced from the host to give up through ace_set_test_hooks: no
+    polls, and the other epilogues sleep ~0.1 ms before they publish; every
+    kernel still exits normally.  A loss
     is then NaN (or the right one, if every word had arrived), the per-bin
     outputs are unaffected, the late words find their abandoned marks and
     clear them, so the workspace is all zero after every call, and the next
@@ -76,20 +76,20 @@ def test_abandoned_loss_words_leave_the_workspace_zero(monkeypatch, binning) -> 
     stream = torch.cuda.current_stream().cuda_stream
     ws = common._WORKSPACES[("cuda", torch.cuda.current_device(), stream)]
     say(f"abandoned loss words {binning}: 50 forwards with no polls and delayed words")
-    monkeypatch.setenv("ACE_FWD_MAX_POLLS", "0")
-    monkeypatch.setenv("ACE_FWD_PUBLISH_DELAY", "2000")
+    _lib.check(_lib.lib().ace_set_test_hooks(0, 2000), "ace_set_test_hooks")
     nan = 0
-    for _ in range(50):
-        loss, coef, d, _, _, _ = hip.hip_forward(pl, cfg)
-        torch.cuda.synchronize()
-        assert torch.equal(coef, want_coef) and torch.equal(d, want_d)
-        if torch.isnan(loss):
-            nan += 1
-        else:
-            assert torch.equal(loss, want_loss)
-        assert int(torch.count_nonzero(ws)) == 0
-    monkeypatch.delenv("ACE_FWD_MAX_POLLS")
-    monkeypatch.delenv("ACE_FWD_PUBLISH_DELAY")
+    try:
+        for _ in range(50):
+            loss, coef, d, _, _, _ = hip.hip_forward(pl, cfg)
+            torch.cuda.synchronize()
+            assert torch.equal(coef, want_coef) and torch.equal(d, want_d)
+            if torch.isnan(loss):
+                nan += 1
+            else:
+                assert torch.equal(loss, want_loss)
+            assert int(torch.count_nonzero(ws)) == 0
+    finally:
+        _lib.check(_lib.lib().ace_set_test_hooks(-1, -1), "ace_set_test_hooks")
     say(f"abandoned loss words {binning}: {nan} of 50 gave up; normal call")
     assert nan > 0  # the give-up path ran
     loss, coef, d, _, _, _ = hip.hip_forward(pl, cfg)

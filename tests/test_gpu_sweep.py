@@ -21,7 +21,7 @@ import pytest
 import torch
 
 from ace_kernels import ACEConfig
-from gpu_helpers import LOSS_ATOL, LOSS_RTOL, assert_grad_close, assert_lowp_grad_close, run, say
+from gpu_helpers import LOSS_ATOL, LOSS_RTOL, assert_grad_close, assert_lowp_grad_close, run, say, truth64
 
 pytestmark = pytest.mark.gpu
 
@@ -87,7 +87,7 @@ def test_sweep(i, b, c, spatial, dtype, kw) -> None:
         return
     voxels = x[0, 0].numel()
     if cfg.binning == "soft" and voxels < 8 * cfg.num_bins:
-        _, grad64 = run("reference", x.double(), y, cfg)
+        _, grad64 = truth64(x, y, cfg)
         assert_grad_close(grad, grad_ref, x, cfg, rtol=1e-3, truth=grad64)
     else:
         assert_grad_close(grad, grad_ref, x, cfg)

@@ -104,6 +104,64 @@ def test_noalloc_matches_forward_on_two_calls(name: str) -> None:
                 f"{name} call {i}: {what}"
 
 
+def _noalloc_call(pl, config, outs, stream):
+    """One ace_forward_noalloc call into preallocated outputs (no checks, no
+    synchronisation: it may be captured)."""
+    coef, d, jac, per_class, loss, st = outs
+    weights = class_weights(config, pl.CL)
+    cw = class_weight_tensor(tuple(weights), pl.x.device) if weights is not None else None
+    return _lib.lib().ace_forward_noalloc(
+        pl.x.data_ptr(), pl.dtype_code, pl.target.data_ptr(), pl.target_kind,
+        pl.B, pl.C, pl.N, pl.K, _lib.SOFT if pl.soft else _lib.HARD, pl.act,
+        int(pl.include_bg), int(config.ignore_empty_classes), hip._REDUCTIONS[config.reduction],
+        int(pl.right), float(config.empty_weight), hip._ptr(cw), pl.btab.data_ptr(), hip._ptr(pl.rtab),
+        coef.data_ptr(), d.data_ptr(), jac.data_ptr(), per_class.data_ptr(), hip._ptr(loss),
+        st.data_ptr(), stream)
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_noalloc_replays_under_graph_capture(binning: str) -> None:
+    """The main use of the entry point: captured into a HIP graph after one
+    warm call, each replay (with eager work and synchronisations between the
+    replays) equals ace_forward bit for bit, and a warm eager call leaves the
+    device's free memory unchanged."""
+    config = ACEConfig(binning=binning, to_onehot_y=True)
+    x, y = _inputs(2, 4, (40, 40, 40), 61)
+    pl = hip.make_plan(x, y, config)
+    want = hip.hip_forward(pl, config, stats=True, shared=False)
+    dev = x.device
+    outs = (torch.empty((pl.B, pl.CL, pl.K), device=dev), torch.empty((pl.B, pl.CL, pl.K), device=dev),
+            torch.empty((pl.B, pl.CL), device=dev), torch.empty((pl.B, pl.CL), device=dev),
+            torch.empty((), device=dev), torch.empty((3, pl.B, pl.CL, pl.K), dtype=torch.float64, device=dev))
+    say(f"noalloc graph {binning}: warm call")
+    _lib.check(_noalloc_call(pl, config, outs, hip._stream(dev)), "ace_forward_noalloc")
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info(dev)[0]
+    _lib.check(_noalloc_call(pl, config, outs, hip._stream(dev)), "ace_forward_noalloc")
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(dev)[0] == free_before
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    say(f"noalloc graph {binning}: capture")
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = _noalloc_call(pl, config, outs, hip._stream(dev))
+    torch.cuda.synchronize()
+    _lib.check(rc, "ace_forward_noalloc (captured)")
+    for r in range(3):
+        for o in outs:
+            o.fill_(7.0)
+        say(f"noalloc graph {binning}: replay {r}")
+        graph.replay()
+        torch.cuda.synchronize()
+        hip.hip_forward(pl, config, stats=True, shared=False)  # eager work between replays
+        torch.cuda.synchronize()
+        got = (outs[4], outs[0], outs[1], outs[2], outs[3], outs[5])
+        for what, g, w in zip(("loss", "coef", "d", "jac", "per_class", "stats"), got, want):
+            assert torch.equal(g, w), f"replay {r}: {what}"
+
+
 def test_noalloc_rejects_oversize_on_the_device() -> None:
     """A problem beyond the scratch returns ACE_ESCRATCH and launches nothing."""
     config = ACEConfig(binning="soft", num_bins=50, to_onehot_y=True)
