@@ -175,7 +175,8 @@ ACE_HD MomentScale moment_scale(int num_bins) {
 
 // Right shift of the per-copy sums of u^2 before they are added into the
 // final sums of a batch index of N voxels: u^2 < 2^48, one copy holds at
-// most 2047 voxels (< 2^59), and N 2^48 / 2^shift < 2^62.
+// most 4095 voxels (< 2^60), a block's tile fewer than 2^15 (below N unless
+// N >= 2^14, where the shift is at least 1), and N 2^48 / 2^shift < 2^62.
 ACE_HD int moment_shift(long long voxels) {
   int bits = 0;
   while (bits < 62 && (1ll << bits) <= voxels) ++bits;  // bit length of N

@@ -46,6 +46,14 @@ enum { kTgtLabels = 0, kTgtOnehot = 1 };
 //   bits [ 0, 42): sum of p in 30-bit fixed point (|sum| < 2^11)
 constexpr int kShiftN = 53;
 constexpr int kShiftG = 42;
+// Soft moments' packed word: count | labelled count | sum u, with
+// u < 2^24 per voxel (moment_scale), so 40 bits hold the sum of
+// kMaxMomCopyCount voxels and the counts take 12 bits each.
+//   bits [52, 64): voxels in the half-bin (<= 4095 per copy and block)
+//   bits [40, 52): of them, voxels labelled with this channel
+//   bits [ 0, 40): sum of u
+constexpr int kMomShiftN = 52;
+constexpr int kMomShiftG = 40;
 
 struct FwdParams {
   const void* x;
@@ -939,20 +947,22 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
 // sum p): counts unscaled, sum p signed (probabilities outside [0, 1] without
 // an activation) -- the upper fields are rounded so that it decodes in
 // [-2^41, 2^41).
+template <int SN = kShiftN, int SG = kShiftG>
 __device__ __forceinline__ void decode_packed(unsigned long long a, long long& n, long long& g,
                                               long long& sp) {
-  const unsigned long long hi = (a + (1ull << (kShiftG - 1))) >> kShiftG;
-  n += (long long)(hi >> (kShiftN - kShiftG));
-  g += (long long)(hi & ((1ull << (kShiftN - kShiftG)) - 1));
-  sp += (long long)(a - (hi << kShiftG));
+  const unsigned long long hi = (a + (1ull << (SG - 1))) >> SG;
+  n += (long long)(hi >> (SN - SG));
+  g += (long long)(hi & ((1ull << (SN - SG)) - 1));
+  sp += (long long)(a - (hi << SG));
 }
 
 // Copies one lane loads before adding them: bounds the registers the block
 // sums hold (the kernel's register count is that of its widest phase).
 constexpr int kSumBatch = 8;
 
-// Sum of the R packed copies starting at w0 (skew s), decoded every `chunk`.
-template <int R, int BATCH = kSumBatch>
+// Sum of the R packed copies starting at w0 (skew s), decoded every `chunk`;
+// MOM: the soft moments' layout (kMomShiftN, kMomShiftG).
+template <int R, int BATCH = kSumBatch, bool MOM = false>
 __device__ __forceinline__ void sum_packed(const unsigned long long* a, int w0, int s, int chunk,
                                            long long& n, long long& g, long long& sp) {
   constexpr int NB = R < BATCH ? R : BATCH;
@@ -966,7 +976,10 @@ __device__ __forceinline__ void sum_packed(const unsigned long long* a, int w0, 
     for (int j = 0; j < NB; ++j) {
       acc += v[j];
       if (((r0 + j + 1) & (chunk - 1)) == 0) {
-        decode_packed(acc, n, g, sp);
+        if constexpr (MOM)
+          decode_packed<kMomShiftN, kMomShiftG>(acc, n, g, sp);
+        else
+          decode_packed(acc, n, g, sp);
         acc = 0;
       }
     }
@@ -1019,7 +1032,7 @@ __device__ __forceinline__ void block_moments_r(const FwdParams& P, const Hist& 
   for (int t = threadIdx.x; t < H2; t += kThreads) {
     long long m[5] = {0, 0, 0, 0, 0};
     // three arrays: half batches keep the registers of the main loop's
-    sum_packed<R, kSumBatch / 2>(H.a, t * R, t, chunk, m[0], m[1], m[2]);
+    sum_packed<R, kSumBatch / 2, true>(H.a, t * R, t, chunk, m[0], m[1], m[2]);
     m[3] = sum_copies_shifted<R, kSumBatch / 2>(H.m2, t * R, t, P.mshift);
     m[4] = sum_copies<R, kSumBatch / 2>(H.mg, t * R, t);
 #pragma unroll
@@ -1703,8 +1716,8 @@ __device__ __forceinline__ void soft_accumulate(const FastTile<C, VEC>& t, const
         const int h = bucket_fix<RIGHT>(g[jj][c], BATCH ? e[jj][c] : tab[g[jj][c] + 1], p[jj][c]);
         const uint32_t u = mad_i24(h, nw, cvt_u32(p[jj][c]));
         const bool hit = lab[jj] == (uint32_t)c;
-        const uint32_t hi = hit ? ((1u << (kShiftN - 32)) | (1u << (kShiftG - 32)))
-                                : (1u << (kShiftN - 32));
+        const uint32_t hi = hit ? ((1u << (kMomShiftN - 32)) | (1u << (kMomShiftG - 32)))
+                                : (1u << (kMomShiftN - 32));
         unsigned long long* a = bin_at(hb[c], h, lsh);
         lds_add(a, ((unsigned long long)hi << 32) | u);
         lds_add(a + words, square_u24(u));

@@ -13,6 +13,7 @@ constexpr int kFrac = 30;               // fixed-point fraction bits of the sums
 constexpr int kMaxChannels = 64;        // largest C with a built kernel
 constexpr size_t kMaxHistLds = 32 * 1024;  // default LDS budget of the histogram copies
 constexpr int kMaxCopyCount = 2047;        // hard: voxels one copy may count (11-bit field)
+constexpr int kMaxMomCopyCount = 4095;     // soft moments: the same (12-bit field)
 constexpr int kCtrStride = 64;             // ints between ticket counters (one 256-byte line each)
 constexpr int kGroupTiles = 16;            // blocks per ticket group
 constexpr int kSingleTicketTiles = 256;    // up to this many blocks per batch index: one ticket level
@@ -225,9 +226,10 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
     if (steps < 1) steps = 1;
     if (steps > 64) steps = 64;
   }
+  const int64_t copy_cap = moments ? kMaxMomCopyCount : kMaxCopyCount;
   if (counted) {
-    // every copy counts at most kMaxCopyCount voxels of a tile
-    const int64_t max_steps = (int64_t)kMaxCopyCount * copies / step_vox;
+    // every copy counts at most copy_cap voxels of a tile
+    const int64_t max_steps = copy_cap * copies / step_vox;
     if (steps > max_steps) steps = (int)(max_steps > 0 ? max_steps : 1);
   }
   g.steps = steps;
@@ -236,7 +238,7 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   // most nt / copies lanes x steps x vec voxels)
   const int64_t copy_vox = (int64_t)(g.nt / copies) * steps * g.var.vec;
   int chunk = copies;
-  while (chunk > 1 && (!soft || moments) && chunk * copy_vox > kMaxCopyCount) chunk /= 2;
+  while (chunk > 1 && (!soft || moments) && chunk * copy_vox > copy_cap) chunk /= 2;
   int lchunk = 0;
   while ((1 << lchunk) < chunk) ++lchunk;
   g.lchunk = lchunk;
