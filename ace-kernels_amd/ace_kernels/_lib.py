@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # enums of include/ace_hip.h
 F32, BF16, F16, F64 = 0, 1, 2, 3
@@ -33,6 +33,9 @@ EXPORTS = (
     "ace_backward",
     "ace_set_launch_events",
     "ace_set_test_hooks",
+    "ace_read_bytes_scratch",
+    "ace_read_bytes",
+    "ace_set_timeline",
     "ace_workspace_bytes_levels",
     "ace_forward_levels",
     "ace_backward_levels",
@@ -162,10 +165,39 @@ def lib() -> ctypes.CDLL:
     handle.ace_set_launch_events.argtypes = [_p, _p]
     handle.ace_set_test_hooks.restype = _i
     handle.ace_set_test_hooks.argtypes = [_i, _i]
+    handle.ace_read_bytes_scratch.restype = _sz
+    handle.ace_read_bytes_scratch.argtypes = []
+    handle.ace_read_bytes.restype = _i
+    handle.ace_read_bytes.argtypes = [_p, _sz, _p, _sz, _p, _p]
+    handle.ace_set_timeline.restype = _i
+    handle.ace_set_timeline.argtypes = [_p]
     version = handle.ace_abi_version()
     if version != ABI_VERSION:
         raise AceLibraryError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}: rebuild it")
     return handle
+
+
+@lru_cache(maxsize=1)
+def autograd():
+    """``ace_kernels._ace_autograd`` (the loss call and its backward node in
+    C++, ``csrc/ace_autograd.cpp``), wired to this process's
+    ``libace_hip.so``: it calls the entry points of the library ``lib()``
+    loaded.  Raises ``AceLibraryError`` when the module is not built."""
+    handle = lib()
+    try:
+        from ace_kernels import _ace_autograd as mod
+    except ImportError as e:
+        raise AceLibraryError(
+            f"ace_kernels/_ace_autograd.so failed to load ({e}): "
+            "run `python ace-kernels_amd/build.py`"
+        ) from e
+
+    def addr(fn) -> int:
+        return int(ctypes.cast(fn, ctypes.c_void_p).value)
+
+    mod.set_entry_points(addr(handle.ace_forward), addr(handle.ace_backward),
+                         addr(handle.ace_error_string))
+    return mod
 
 
 def check(rc: int, what: str) -> None:

@@ -26,12 +26,12 @@ path.  Their targets are int64 class indices or a float64 one-hot.
 from __future__ import annotations
 
 from functools import lru_cache
-from typing import Any, Optional, Tuple
+from typing import Any, Dict, Optional, Tuple
 
 import torch
 
 from ace_kernels import _lib
-from ace_kernels.common import bin_tables, class_weight_tensor, class_weights, workspace
+from ace_kernels.common import bin_tables, capturing, class_weight_tensor, class_weights, workspace
 from ace_kernels.config import ACEConfig
 from ace_kernels.registry import register
 
@@ -224,20 +224,70 @@ def hip_backward(pl: Plan, coef: torch.Tensor, d: torch.Tensor, jac: torch.Tenso
     return dx.view(pl.in_shape)
 
 
+class _Call:
+    """A call signature -- (configuration, input shape and dtype, target
+    shape and dtype, devices, stream) -- whose arguments of ``ace_forward`` /
+    ``ace_backward`` are fixed, held by the C++ loss call
+    (``_ace_autograd.Signature``): a call of that signature allocates its
+    outputs, launches the forward and records the backward node in C++
+    (``csrc/ace_autograd.cpp``), with no Python autograd Function.
+
+    A signature qualifies when its kernel views are the caller's own tensors
+    (contiguous, no dtype conversion) and the input is not float64 (its own
+    entry points); it is remembered after its first call has succeeded.
+    coef, d and jac (and the per-class errors, unless they are the returned
+    loss) share one float32 allocation; the loss has its own (the caller may
+    modify it in place).  The workspace is the stream's when the signature
+    is made: a buffer that a larger problem later replaces is retired, never
+    freed, and stays zero between calls on its stream."""
+
+    __slots__ = ("sig", "ws", "tables")
+
+
+def _build_call(pl: Plan, config: ACEConfig, stream: int) -> Optional[_Call]:
+    if pl.dtype_code == _lib.F64:
+        return None
+    dev = pl.x.device
+    binning = _lib.SOFT if pl.soft else _lib.HARD
+    dims = (pl.B, pl.C, pl.N, pl.K, binning, pl.dtype_code, int(pl.include_bg), pl.target_kind)
+    ws = workspace(dev, stream, _workspace_bytes(dims))
+    weights = class_weights(config, pl.CL)
+    cw = class_weight_tensor(tuple(weights), dev) if weights is not None else None
+    bck, bc = pl.B * pl.CL * pl.K, pl.B * pl.CL
+    reduction = _REDUCTIONS[config.reduction]
+    reduced = reduction != _lib.RED_NONE
+    c = _Call()
+    c.sig = _lib.autograd().make_signature(
+        pl.dtype_code, pl.target_kind, pl.B, pl.C, pl.N, pl.K, binning, pl.act, int(pl.include_bg),
+        int(config.ignore_empty_classes), reduction, int(pl.right), float(config.empty_weight),
+        _ptr(cw) or 0, pl.btab.data_ptr(), _ptr(pl.rtab) or 0, ws.data_ptr(), ws.numel(),
+        2 * bck + bc + (bc if reduced else 0), 4 * bck, 8 * bck, 4 * (2 * bck + bc), reduced, pl.soft,
+        [] if reduced else [pl.B, pl.CL, *([1] * pl.spatial_ndim)])
+    c.ws, c.tables = ws, (cw, pl.btab, pl.rtab)  # kept alive with the signature
+    return c
+
+
+# signature -> _Call (None: the general path); bounded, cleared when full
+_CALLS: Dict[Tuple[Any, ...], Optional[_Call]] = {}
+_MAX_CALLS = 256
+
+
 class _HipACELoss(torch.autograd.Function):
+    """The general path: calls that no remembered signature covers."""
+
     @staticmethod
-    def forward(ctx: Any, input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> torch.Tensor:
-        pl = make_plan(input, target, config)
+    def forward(ctx: Any, input: torch.Tensor, target: torch.Tensor, config: ACEConfig,
+                pl: Plan) -> torch.Tensor:
         loss, coef, d, jac, _, _ = hip_forward(pl, config)
-        # the kernel views of input / target go through save_for_backward (same
-        # storage as the caller's tensors; version-checked by autograd)
-        ctx.save_for_backward(pl.x, pl.target, coef, d, jac)
+        # the kernel views of input / target (same storage and version counter
+        # as the caller's tensors) go through save_for_backward
+        ctx.save_for_backward(pl.x.detach(), pl.target.detach(), coef, d, jac)
         pl.x = pl.target = None
         ctx.plan = pl
         return loss
 
     @staticmethod
-    def backward(ctx: Any, grad_output: torch.Tensor) -> Tuple[Optional[torch.Tensor], None, None]:
+    def backward(ctx: Any, grad_output: torch.Tensor) -> Tuple[Optional[torch.Tensor], None, None, None]:
         x, target, coef, d, jac = ctx.saved_tensors
         pl = ctx.plan
         pl.x, pl.target = x, target
@@ -245,12 +295,36 @@ class _HipACELoss(torch.autograd.Function):
             dx = hip_backward(pl, coef, d, jac, grad_output)
         finally:
             pl.x = pl.target = None
-        return dx, None, None
+        return dx, None, None, None
 
 
 def hip_ace(input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> torch.Tensor:
-    """Registry entry ``fn(input, target, config) -> loss``."""
-    loss: torch.Tensor = _HipACELoss.apply(input, target, config)
+    """Registry entry ``fn(input, target, config) -> loss``.
+
+    A remembered signature runs in C++ (``_Call``); any other call builds a
+    ``Plan`` and runs the autograd Function above (or, with no gradient to
+    record, the forward alone), and remembers its signature once it has
+    succeeded."""
+    stream = _stream(input.device) if input.is_cuda else 0
+    key = (config, input.shape, input.dtype, target.shape, target.dtype, input.get_device(),
+           target.get_device(), stream)
+    call = _CALLS.get(key)
+    if call is not None and input.is_contiguous() and target.is_contiguous():
+        loss: torch.Tensor = _lib.autograd().ace_loss(input, target, call.sig)
+        return loss
+    pl = make_plan(input, target, config)
+    own = (pl.x.data_ptr() == input.data_ptr() and pl.x.dtype == input.dtype and input.is_contiguous()
+           and pl.target.data_ptr() == target.data_ptr() and pl.target.dtype == target.dtype
+           and target.is_contiguous())
+    if torch.is_grad_enabled() and input.requires_grad:
+        loss = _HipACELoss.apply(input, target, config, pl)
+    else:
+        loss = hip_forward(pl, config)[0]
+    if key not in _CALLS and not capturing(input.device):
+        if len(_CALLS) >= _MAX_CALLS:
+            _CALLS.clear()
+        pl.x, pl.target = input, target  # for _build_call: device, tables (kernel views not needed)
+        _CALLS[key] = _build_call(pl, config, stream) if own else None
     return loss
 
 

@@ -1,4 +1,6 @@
-"""Build libace_hip.so (the C-ABI of the HIP kernels) for gfx950 with hipcc.
+"""Build libace_hip.so (the C-ABI of the HIP kernels) for gfx950 with hipcc,
+and _ace_autograd.so (the loss call and its backward node in C++ over that
+C-ABI) with g++ against torch's headers.
 
     python ace-kernels_amd/build.py            # compile + link
     python ace-kernels_amd/build.py --check    # also print kernel resource usage
@@ -27,6 +29,8 @@ CSRC = HERE / "csrc"
 INCLUDE = ROOT / "include"
 OUT_DIR = HERE / "ace_kernels"
 LIB = OUT_DIR / "libace_hip.so"
+AUTOGRAD_SRC = CSRC / "ace_autograd.cpp"
+AUTOGRAD_LIB = OUT_DIR / "_ace_autograd.so"
 OBJ_DIR = HERE / "_build"
 
 ARCH = os.environ.get("ACE_OFFLOAD_ARCH", "gfx950")
@@ -67,15 +71,52 @@ def _compile(src: Path, extra: list, incremental: bool = False) -> Path:
     return obj
 
 
+def _build_autograd(incremental: bool = False) -> Path:
+    """g++ -shared ace_autograd.cpp -> ace_kernels/_ace_autograd.so (a Python
+    extension module: pybind11 and torch's headers; host code only, it calls
+    libace_hip.so through entry points handed over at load time)."""
+    out = AUTOGRAD_LIB
+    if incremental and out.exists():
+        deps = [AUTOGRAD_SRC, *INCLUDE.glob("*.h")]
+        if out.stat().st_mtime > max(d.stat().st_mtime for d in deps):
+            return out
+    import sysconfig
+
+    import torch
+    from torch.utils.cpp_extension import include_paths
+
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+        str(AUTOGRAD_SRC), "-o", str(tmp),
+        f"-I{sysconfig.get_paths()['include']}", *(f"-I{p}" for p in include_paths()),
+        f"-I{INCLUDE}", "-I/opt/rocm/include",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DTORCH_EXTENSION_NAME=_ace_autograd", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+        f"-Wl,-rpath,{torch_lib}",
+    ]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed for {AUTOGRAD_SRC.name}:\n{' '.join(cmd)}\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False, extra: list | None = None, incremental: bool = False) -> Path:
-    """Compile every csrc/*.hip and link ace_kernels/libace_hip.so; return its path.
+    """Compile every csrc/*.hip and link ace_kernels/libace_hip.so, and build
+    ace_kernels/_ace_autograd.so; return the library's path.
     ``incremental``: skip objects newer than their source and every header."""
     extra = list(extra or [])
     OBJ_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
-    jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    jobs = min(len(sources) + 1, max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(jobs) as pool:
+        autograd = pool.submit(_build_autograd, incremental)
         objs = list(pool.map(lambda s: _compile(s, extra, incremental), sources))
+        autograd.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -83,7 +124,7 @@ def build(verbose: bool = False, extra: list | None = None, incremental: bool = 
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stderr}")
     os.replace(tmp, LIB)
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources")
+        print(f"built {LIB} from {len(sources)} sources, and {AUTOGRAD_LIB}")
     return LIB
 
 

@@ -140,6 +140,8 @@ bool fast_forward(bool soft, bool labels, int act, int64_t channels, bool moment
 // before a batch epilogue publishes its word (0), so that a test can make
 // that wait give up.
 std::atomic<int> g_max_polls{kMaxPolls};
+// ace_set_timeline's buffer (null: no stamps), process-wide
+std::atomic<unsigned long long*> g_timeline{nullptr};
 std::atomic<int> g_publish_delay{0};
 
 // Forward geometry of one problem (the kernel the launcher will pick).
@@ -251,6 +253,7 @@ FwdParams fwd_params(const void* x, int x_dtype, const void* target, bool labels
   p.red = reduction;
   p.empty_w = empty_weight;
   p.packed = g.packed ? 1 : 0;
+  p.tl = g_timeline.load(std::memory_order_relaxed);
   p.max_polls = g_max_polls.load(std::memory_order_relaxed);
   p.publish_delay = g_publish_delay.load(std::memory_order_relaxed);
   p.pscale = 1.0 / 1073741824.0;  // the generic kernels' sums: 30-bit fixed point
@@ -394,6 +397,34 @@ __global__ void __launch_bounds__(kThreads) clear_words(unsigned long long* p, s
   for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < words; i += stride) p[i] = 0ull;
 }
 
+// ace_read_bytes: every 16-byte vector of a and b read once (grid-stride,
+// four vectors in flight per lane) and folded into a per-lane xor.
+// kFastThreads-thread blocks, the forward's widest.
+constexpr int kReadBlocks = 512;
+__global__ void __launch_bounds__(kFastThreads) read_bytes_kernel(const uint4* a, size_t na,
+                                                                   const uint4* b, size_t nb,
+                                                                   unsigned* out) {
+  const size_t stride = (size_t)gridDim.x * kFastThreads;
+  unsigned acc = 0;
+  for (int buf = 0; buf < 2; ++buf) {
+    const uint4* p = buf == 0 ? a : b;
+    const size_t n = buf == 0 ? na : nb;
+    size_t i = (size_t)blockIdx.x * kFastThreads + threadIdx.x;
+    for (; i + 3 * stride < n; i += 4 * stride) {
+      const uint4 v0 = p[i], v1 = p[i + stride], v2 = p[i + 2 * stride], v3 = p[i + 3 * stride];
+      acc ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
+      acc ^= v2.x ^ v2.y ^ v2.z ^ v2.w ^ v3.x ^ v3.y ^ v3.z ^ v3.w;
+    }
+    for (; i < n; i += stride) {
+      const uint4 v = p[i];
+      acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+  }
+  // a store that depends on every lane's loads (and almost never happens), so
+  // that no load is dead; the scratch word's value means nothing
+  if (acc == 0x2545f491u) out[blockIdx.x] = acc;
+}
+
 }  // namespace
 }  // namespace ace
 
@@ -409,7 +440,7 @@ using namespace ace;
 
 extern "C" {
 
-int ace_abi_version(void) { return 7; }
+int ace_abi_version(void) { return 8; }
 
 const char* ace_error_string(int code) {
   switch (code) {
@@ -672,6 +703,33 @@ int ace_forward_noalloc(const void* x, int x_dtype, const void* target, int targ
 int ace_set_launch_events(void* start, void* stop) {
   launch_events() = LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
   return ACE_OK;
+}
+
+int ace_set_timeline(void* stamps) {
+  g_timeline.store(static_cast<unsigned long long*>(stamps), std::memory_order_relaxed);
+  return ACE_OK;
+}
+
+size_t ace_read_bytes_scratch(void) { return kReadBlocks * sizeof(unsigned); }
+
+int ace_read_bytes(const void* a, size_t a_bytes, const void* b, size_t b_bytes, void* scratch,
+                   void* stream) {
+  if ((!a && a_bytes) || (!b && b_bytes) || !scratch) return ACE_EINVAL;
+  if (!aligned_to(a, 16) || !aligned_to(b, 16) || (a_bytes % 16) || (b_bytes % 16)) return ACE_EINVAL;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const LaunchEvents& ev = launch_events();
+  const uint4* pa = static_cast<const uint4*>(a);
+  const uint4* pb = static_cast<const uint4*>(b);
+  const size_t na = a_bytes / 16, nb = b_bytes / 16;
+  unsigned* out = static_cast<unsigned*>(scratch);
+  if (ev.start || ev.stop) {
+    void* args[] = {&pa, const_cast<size_t*>(&na), &pb, const_cast<size_t*>(&nb), &out};
+    return to_code(hipExtLaunchKernel(reinterpret_cast<const void*>(read_bytes_kernel),
+                                      dim3(kReadBlocks), dim3(kFastThreads), args, 0, s, ev.start,
+                                      ev.stop, 0));
+  }
+  hipLaunchKernelGGL(read_bytes_kernel, dim3(kReadBlocks), dim3(kFastThreads), 0, s, pa, na, pb, nb, out);
+  return to_code(hipGetLastError());
 }
 
 int ace_set_test_hooks(int max_polls, int publish_delay) {

@@ -100,7 +100,20 @@ struct FwdParams {
   float* f;
   float* loss;
   double* stats;
+  // timeline (ace_set_timeline; null otherwise): per block, 8 stamps of the
+  // 100 MHz clock (s_memrealtime) at the phases of fast_stamp
+  unsigned long long* tl;
 };
+
+// Phases a fast forward block stamps into FwdParams::tl (thread 0, vector
+// stores): start, main loop done, block sums and their final-sum atomics
+// done, ticket drawn, and in an epilogue block its float64 terms (soft
+// moments), its bins, its end and the loss.
+enum { kTlStart = 0, kTlLoop, kTlSums, kTlTicket, kTlEpiEnd, kTlLoss, kTlEpiTerms, kTlEpiBins };
+__device__ __forceinline__ void fast_stamp(const FwdParams& P, int phase) {
+  if (P.tl && threadIdx.x == 0)
+    P.tl[(size_t)blockIdx.x * 8 + phase] = __builtin_amdgcn_s_memrealtime();
+}
 
 // Soft moments fixed point in the main loop: p scaled by sc = 2^m (isc =
 // 2^-m); nw = -w (the half-bin base is h w).
@@ -752,6 +765,7 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
                    (double)m[4] * mscale, L, (double)repl[hh], (double)repl[hh + 2], terms + 6 * t);
     }
     __syncthreads();
+    fast_stamp(P, kTlEpiTerms);
   }
   // per bin: W, P, G (final sums, or the half-bin terms of soft moments),
   // then d; without moments two bins per thread and pass, both bins' loads
@@ -843,6 +857,7 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
     }
   }
   __syncthreads();
+  fast_stamp(P, kTlEpiBins);
   // class rows: K <= 64 bins per row take one lane each, 64 / seg rows per
   // wave (seg = 16, 32 or 64 lanes per row); longer rows loop over a wave
   const int lane = tid & 63;
@@ -1121,6 +1136,7 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
   __shared__ int s_last;
   wait_own_writes();
   __syncthreads();
+  fast_stamp(P, kTlSums);
   if (tid == 0) {
     const int64_t g = tile / P.gs;
     const int64_t gsize = min(P.gs, P.tiles - g * P.gs);
@@ -1143,6 +1159,7 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
     s_last = last;
   }
   __syncthreads();
+  fast_stamp(P, kTlTicket);
   if (!s_last) return;
   const int rows = P.B * CL;
   if (P.epi_all) {
@@ -1166,6 +1183,7 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
   int* tc = counter(P, (int64_t)P.B * P.gpb + P.B);
   if (tid == 0 && P.red != kRedNone) lt = ticket(tc);
   const float total = epilogue<SOFT, MOM>(P, hist, repl, CK, CL, b, 1);
+  fast_stamp(P, kTlEpiEnd);
   if (P.red == kRedNone || tid >= 64) return;
   // wave 0, every lane active: thread 0's ticket and partial sum
   const bool last = __builtin_amdgcn_readfirstlane(lt) == P.B - 1;
@@ -1203,6 +1221,7 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
     sum += wave_sum(v);
   }
   if (tid == 0) P.loss[0] = P.red == kRedMean ? sum / (float)rows : sum;
+  fast_stamp(P, kTlLoss);
 }
 
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
@@ -1802,6 +1821,7 @@ __device__ __forceinline__ void fast_accumulate(const FastTile<C, VEC>& t, const
 template <typename T, int C, int VEC, bool SOFT, bool RIGHT, bool SKIP0>
 __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t blk,
                                               unsigned char* smem) {
+  fast_stamp(P, kTlStart);
   float* tabs = reinterpret_cast<float*>(smem);
   const int K = P.K;
   const int n = SOFT ? 2 * K : K;
@@ -1907,6 +1927,7 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
   // the block's sums and the cross-block protocol take kThreads threads; the
   // other waves end here (a barrier waits only for waves that have not ended)
   if (tid >= kThreads) return;
+  fast_stamp(P, kTlLoop);
   fwd_finish<SOFT, SOFT>(P, H, hist, repl, CK, CL, b, tile, true);
 }
 

@@ -138,7 +138,8 @@ def time_kernel_steps(fn, steps: int, warmup: int, flush):
 
 
 def time_back_to_back(fn, launches: int, warmup: int):
-    """Mean ms per call of ``fn`` issued back to back (events around the loop)."""
+    """Mean ms per call of ``fn`` issued back to back with no flush: the
+    steady state of a training loop, whose device time hides the host's."""
     import torch
 
     for _ in range(warmup):
@@ -152,6 +153,71 @@ def time_back_to_back(fn, launches: int, warmup: int):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / launches
+
+
+def read_ceiling(tensors, steps: int, warmup: int, flush):
+    """Cold read of the same bytes as the forward kernel, timed the same way:
+    ``ace_read_bytes`` (a plain streaming read, every byte once) with
+    kernel-stamped events after the 1 GiB flush; and a torch reduction of the
+    same tensors, timed by events recorded on the stream."""
+    import torch
+
+    from ace_kernels import _lib
+    from ace_kernels.impls import hip_mi355x as hip
+
+    lib = _lib.lib()
+    a, b = tensors
+    scratch = torch.empty(lib.ace_read_bytes_scratch(), dtype=torch.uint8, device=a.device)
+    na, nb = a.numel() * a.element_size(), b.numel() * b.element_size()
+
+    def read():
+        _lib.check(lib.ace_read_bytes(a.data_ptr(), na, b.data_ptr(), nb, scratch.data_ptr(),
+                                      hip._stream(a.device)), "ace_read_bytes")
+
+    kern = time_kernel_steps(read, steps, warmup, flush)
+    torch_ms = time_steps(lambda: (a.sum(), b.sum()), steps, warmup, flush)
+    ms = statistics.median(kern)
+    return {"bytes": na + nb, "ms_p50": ms, "GBps": (na + nb) / (ms * 1e-3) / 1e9,
+            "frac_of_peak": (na + nb) / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+            "torch_sum_ms_p50_stream_events": statistics.median(torch_ms)}
+
+
+def host_cost(x, y, cfg, calls: int = 200):
+    """Host microseconds per call, each call issued to an idle device
+    (synchronised before, not after: the time is the host's alone); median
+    of ``calls``.  forward: one ``ace_loss`` call with autograd recording;
+    backward: ``autograd.grad`` through that loss (the autograd engine plus
+    the backward launch); step: the two plus the ``.sum()``;
+    torch_floor_step: the same step over ``(x * 1.0).sum()``, the engine's
+    own cost for the simplest differentiable op."""
+    import torch
+
+    from ace_kernels import ace_loss
+
+    def fwd():
+        return ace_loss(x, y, cfg, impl="hip_mi355x")
+
+    loss = fwd()
+    xx = x.detach().clone().requires_grad_(True)
+    fns = {
+        "forward": fwd,
+        "backward": lambda: torch.autograd.grad(loss, x, retain_graph=True),
+        "step": lambda: torch.autograd.grad(fwd().sum(), x),
+        "torch_floor_step": lambda: torch.autograd.grad((xx * 1.0).sum(), xx),
+    }
+    out = {}
+    for name, fn in fns.items():
+        for _ in range(10):
+            fn()
+        ts = []
+        for _ in range(calls):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        torch.cuda.synchronize()
+        out[name] = statistics.median(ts) * 1e6
+    return out
 
 
 def bench_workload(wl, steps: int, warmup: int, flush):
@@ -203,6 +269,9 @@ def bench_workload(wl, steps: int, warmup: int, flush):
     fwd_stream = time_steps(lambda: hip.hip_forward(pl, cfg), steps, warmup, flush)
     fwd_ms = statistics.fmean(fwd_cold)
     bwd_ms = statistics.fmean(bwd_cold)
+    ceiling = read_ceiling((x.detach(), y), steps, warmup, flush)
+    host = host_cost(x, y, cfg)
+    b2b = time_back_to_back(step, 50, 5)
 
     n_vox = wl.batch * wl.voxels
     xb = wl.input_bytes()
@@ -224,6 +293,10 @@ def bench_workload(wl, steps: int, warmup: int, flush):
         "fwd_GBps": wl.ideal_bytes("fwd") / (statistics.median(fwd_cold) * 1e-3) / 1e9,
         "graph_replay_matches_eager": graph_ok,
         "loss": float(loss.item()),
+        "read_ceiling": ceiling,
+        "fwd_frac_of_read_ceiling": (ceiling["ms_p50"] / statistics.median(fwd_cold)),
+        "host_us": host,
+        "back_to_back_ms": b2b,
     }
     p50 = out["eager_ms"]["p50"]
     out["effective_GBps"] = ideal / (p50 * 1e-3) / 1e9
@@ -316,6 +389,9 @@ def bench_deep_supervision(binning: str, steps: int, warmup: int, flush):
             return torch.autograd.grad(ace_loss(x, y, cfg, impl="hip_mi355x").sum(), x)
         per_level[wl.name] = _quantiles(time_steps(one, steps, warmup, flush))["p50"]
     ideal = sum(wl.ideal_bytes("fwd_bwd") for wl in levels)
+    # steady state: steps back to back, no flush (per-level calls, one launch)
+    b2b = {"per_level_calls_ms": time_back_to_back(step, 50, 5),
+           "one_launch_ms": time_back_to_back(step_levels, 50, 5)}
     return {
         "binning": binning,
         "levels": [wl.name for wl in levels],
@@ -327,6 +403,7 @@ def bench_deep_supervision(binning: str, steps: int, warmup: int, flush):
         "one_launch_graph_ms": _quantiles(lv_graphed),
         "one_launch_matches_per_level_calls": lv_ok,
         "level_eager_ms_p50": per_level,
+        "back_to_back_ms": b2b,
         "pct_hbm_peak": 100.0 * ideal / (_quantiles(eager)["p50"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
     }
 
@@ -601,6 +678,71 @@ def summarize_profiles(dirs, workloads) -> int:
     return 0
 
 
+TIMELINE_PHASES = ["block starts", "main loop done", "block sums + final-sum atomics done",
+                   "ticket drawn", "epilogue done (epilogue blocks)", "loss written (last block)",
+                   "moments' float64 terms done (soft epilogue blocks)", "bins done (epilogue blocks)"]
+
+
+def timeline(workloads, launches: int) -> int:
+    """Per-block phase timeline of cold forwards (ace_set_timeline: thread 0
+    of every block of a fast forward kernel stamps the 100 MHz clock at each
+    phase), as a markdown summary: per phase the first, median and last block,
+    in microseconds from the first block's start, median over the launches."""
+    import numpy as np
+    import torch
+
+    from ace_kernels import _lib
+    from ace_kernels.impls import hip_mi355x as hip
+    from ace_kernels.workloads import workload
+
+    lib = _lib.lib()
+    flush = ReadFlush()
+    buf = torch.zeros(65536 * 8, dtype=torch.int64, device="cuda")
+    print(f"Per-block timeline of {launches} cold forward launches per workload (after the "
+          f"1 GiB read flush), us from the first block's start; median over the launches.\n")
+    for idx in workloads:
+        wl = workload(idx)
+        x, y = wl.make("cuda")
+        pl = hip.make_plan(x, y, wl.config)
+        hip.hip_forward(pl, wl.config)
+        torch.cuda.synchronize()
+        per_launch = []
+        for rep in range(launches + 2):
+            flush()
+            buf.zero_()
+            torch.cuda.synchronize()
+            _lib.check(lib.ace_set_timeline(buf.data_ptr()), "ace_set_timeline")
+            try:
+                hip.hip_forward(pl, wl.config)
+            finally:
+                lib.ace_set_timeline(None)
+            torch.cuda.synchronize()
+            if rep < 2:
+                continue
+            t = buf.view(-1, 8).cpu().numpy()
+            nb = int((t[:, 0] > 0).sum())
+            t = t[:nb].astype(np.float64)
+            rel = np.where(t > 0, (t - t[:, 0].min()) / 100.0, np.nan)
+            row = {}
+            for j in range(8):
+                col = rel[:, j][~np.isnan(rel[:, j])]
+                if col.size:
+                    row[j] = (col.min(), float(np.median(col)), col.max(), col.size)
+            per_launch.append((nb, row))
+        nb = per_launch[0][0]
+        print(f"## {wl.name} ({nb} blocks)\n")
+        print("| phase | first block | median block | last block | blocks |")
+        print("|---|---:|---:|---:|---:|")
+        for j in (0, 1, 2, 3, 6, 7, 4, 5):
+            vals = [r[j] for _, r in per_launch if j in r]
+            if not vals:
+                continue
+            a = np.median(np.array([v[:3] for v in vals]), 0)
+            print(f"| {TIMELINE_PHASES[j]} | {a[0]:.2f} | {a[1]:.2f} | {a[2]:.2f} | {vals[0][3]} |")
+        print()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -614,6 +756,8 @@ def main() -> int:
                     help="no live rocprofv3 traffic runs (for runs under a profiler)")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="LAUNCHES",
                     help="only launch the kernels LAUNCHES times each (for rocprofv3)")
+    ap.add_argument("--timeline", type=int, default=0, metavar="LAUNCHES",
+                    help="print the per-block phase timeline of LAUNCHES cold forwards (markdown)")
     ap.add_argument("--summarize-profiles", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc runs of --profile-kernels (no GPU needed)")
     args = ap.parse_args()
@@ -636,6 +780,8 @@ def main() -> int:
     if args.profile_kernels:
         profile_kernels([int(v) for v in args.workloads.split(",")], args.profile_kernels)
         return 0
+    if args.timeline:
+        return timeline([int(v) for v in args.workloads.split(",")], args.timeline)
     flush = ReadFlush()
     results = []
     for idx in [int(v) for v in args.workloads.split(",")]:
@@ -707,7 +853,14 @@ def main() -> int:
             "bytes_per_launch": dom["bytes"],
             "bytes_per_voxel": dom["bytes_per_voxel"],
             "ms_mean": dom["ms"],
+            # the read rate a plain streaming kernel reaches on the forward's
+            # bytes (same cold flush, same kernel-stamped timing)
+            "read_ceiling_GBps": main_r["read_ceiling"]["GBps"],
+            "read_ceiling_frac": main_r["read_ceiling"]["frac_of_peak"],
         },
+        "fwd_frac_of_read_ceiling": main_r["fwd_frac_of_read_ceiling"],
+        "host_us": main_r["host_us"],
+        "back_to_back_ms": main_r["back_to_back_ms"],
         "workloads": results,
         "deep_supervision": deepsup,
         "hard_bin_parity": parity,

@@ -252,6 +252,34 @@ int ace_forward_noalloc(const void* x, int x_dtype, const void* target,
 int ace_set_launch_events(void* start, void* stop);
 
 /*
+ * Measurement only; no counterpart in the reference, whose benchmark tables
+ * each implementation against a bandwidth floor computed from the peak
+ * (src/ace_bench/calculator.py:1-35).  These give the floor the device
+ * actually reaches.
+ *
+ * ace_read_bytes reads every byte of a and b once (16-byte aligned, sizes
+ * multiples of 16) with a plain streaming kernel and nothing else, as an
+ * asynchronous launch on `stream`; `scratch` is device memory of
+ * ace_read_bytes_scratch() bytes, whose contents mean nothing.  Timed like
+ * the forward (ace_set_launch_events, the same cold cache), it is the read
+ * rate a kernel of the forward's bytes can reach.  Returns ACE_EINVAL for
+ * unaligned or null arguments, else ACE_OK or a HIP error.
+ *
+ * ace_set_timeline sets (or clears, with NULL) a device buffer of 8
+ * uint64_t per block into which every later ace_forward launch of a fast
+ * kernel (softmax with class labels) stamps the 100 MHz clock
+ * (s_memrealtime) at its phases: 0 start, 1 main loop done, 2 block sums and
+ * their final-sum atomics done, 3 ticket drawn, and in the blocks that run
+ * an epilogue 4 epilogue done, 5 loss written, 6 soft moments' terms done,
+ * 7 bins done.  The buffer must hold the launch's blocks; process-wide.
+ * Returns ACE_OK.
+ */
+size_t ace_read_bytes_scratch(void);
+int ace_read_bytes(const void* a, size_t a_bytes, const void* b, size_t b_bytes, void* scratch,
+                   void* stream);
+int ace_set_timeline(void* stamps);
+
+/*
  * Test hooks.  No counterpart in the reference: they let a test force the
  * forward's cross-block failure handling from the host, with every kernel
  * still exiting normally.  Process-wide, read by each later forward call.

@@ -206,3 +206,24 @@ def test_f64_entry_points_validate_before_launch() -> None:
     ws = lib.ace_workspace_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F64, 1, 0)
     assert ws > lib.ace_workspace_bytes(2, 4, 128 ** 3, 20, _lib.HARD, _lib.F32, 1, 0) > 0
     assert ws % 256 == 0
+
+
+def test_autograd_module_loads_and_builds_signatures() -> None:
+    """The C++ loss call (``_ace_autograd``) loads beside the library, is
+    wired to its entry points, and builds a signature on the host; the
+    no-GPU check of its calls is that the extension module carries them."""
+    mod = _lib.autograd()
+    for name in ("make_signature", "set_entry_points", "ace_loss", "Signature"):
+        assert hasattr(mod, name), name
+    sig = mod.make_signature(_lib.F32, _lib.TARGET_LABELS_I64, 2, 4, 64, 20, _lib.HARD, _lib.ACT_SOFTMAX,
+                             1, 1, _lib.RED_MEAN, 0, 0.01, 0, 1 << 20, 0, 2 << 20, 1 << 16,
+                             2 * 160 + 8 + 8, 640, 1280, 1312, True, False, [])
+    assert isinstance(sig, mod.Signature)
+
+
+def test_autograd_source_reaches_kernels_through_the_c_abi() -> None:
+    """The C++ loss call includes the C-ABI header and launches nothing itself."""
+    src = (Path(__file__).resolve().parents[1] / "ace-kernels_amd" / "csrc" / "ace_autograd.cpp").read_text()
+    assert '#include "ace_hip.h"' in src
+    for name in ("hipLaunchKernel", "<<<", "hipMalloc", "hipMemset"):
+        assert name not in src, name
