@@ -196,6 +196,7 @@ def autograd():
         return int(ctypes.cast(fn, ctypes.c_void_p).value)
 
     mod.set_entry_points(addr(handle.ace_forward), addr(handle.ace_backward),
+                         addr(handle.ace_forward_levels), addr(handle.ace_backward_levels),
                          addr(handle.ace_error_string))
     return mod
 

@@ -12,17 +12,23 @@ config, impl="hip_mi355x")`` on that level alone.
 Only configurations with a fast kernel: softmax activation, class-index
 targets (``to_onehot_y``), C in {2, 3, 4, 16}, the same batch, channels and
 dtype on every level; anything else raises (call ``ace_loss`` per level).
+
+A levels signature (configuration, every level's input and target shapes
+and dtypes, device, stream) that has run once, with contiguous inputs that
+need no conversion, runs in C++ (``_ace_autograd.ace_loss_levels``: one
+forward launch and one backward node for all levels); other calls run the
+autograd Function below.
 """
 
 from __future__ import annotations
 
 import ctypes
-from typing import Any, List, Optional, Sequence, Tuple
+from typing import Any, Dict, List, Optional, Sequence, Tuple
 
 import torch
 
 from ace_kernels import _lib
-from ace_kernels.common import class_weight_tensor, class_weights, workspace
+from ace_kernels.common import capturing, class_weight_tensor, class_weights, workspace
 from ace_kernels.config import ACEConfig
 from ace_kernels.impls.hip_mi355x import Plan, _ptr, _stream, make_plan
 
@@ -145,6 +151,38 @@ class _HipLevelsLoss(torch.autograd.Function):
         return (None, None, *dxs, *([None] * n))
 
 
+def _level_signature(plans: Sequence[Plan], config: ACEConfig, stream: int):
+    """The C++ levels call's fixed arguments (``_ace_autograd.LevelSignature``)
+    and the buffers they point into (kept alive beside it)."""
+    lib = _lib.lib()
+    p0 = plans[0]
+    dev = p0.x.device
+    binning = _lib.SOFT if p0.soft else _lib.HARD
+    n = len(plans)
+    vox = (ctypes.c_int64 * n)(*[p.N for p in plans])
+    nbytes = lib.ace_workspace_bytes_levels(n, vox, p0.B, p0.C, p0.K, binning, p0.dtype_code,
+                                            int(p0.include_bg))
+    ws = workspace(dev, stream, nbytes)
+    weights = class_weights(config, p0.CL)
+    cw = class_weight_tensor(tuple(weights), dev) if weights is not None else None
+    reduction = _REDUCTIONS[config.reduction]
+    reduced = reduction != _lib.RED_NONE
+    bck, bc = p0.B * p0.CL * p0.K, p0.B * p0.CL
+    sig = _lib.autograd().make_level_signature(
+        p0.dtype_code, p0.B, p0.C, p0.K, binning, int(p0.include_bg), int(config.ignore_empty_classes),
+        reduction, int(p0.right), float(config.empty_weight), _ptr(cw) or 0, p0.btab.data_ptr(),
+        _ptr(p0.rtab) or 0, ws.data_ptr(), ws.numel(), [p.N for p in plans],
+        2 * bck + bc + (bc if reduced else 0), 4 * bck, 8 * bck, 4 * (2 * bck + bc), reduced, p0.soft,
+        [] if reduced else [p0.B, p0.CL, *([1] * p0.spatial_ndim)])
+    return sig, (ws, cw, p0.btab, p0.rtab)
+
+
+# levels signature -> (LevelSignature, kept buffers), or None for the
+# general path; bounded, cleared when full
+_LEVEL_CALLS: Dict[Tuple[Any, ...], Optional[Tuple[Any, Tuple[Any, ...]]]] = {}
+_MAX_LEVEL_CALLS = 64
+
+
 def ace_loss_levels(inputs: Sequence[torch.Tensor], targets: Sequence[torch.Tensor],
                     config: ACEConfig) -> List[torch.Tensor]:
     """The loss of each level (same as ``ace_loss(inputs[i], targets[i], config)``)
@@ -152,4 +190,22 @@ def ace_loss_levels(inputs: Sequence[torch.Tensor], targets: Sequence[torch.Tens
     if len(inputs) != len(targets):
         raise ValueError("one target per input")
     n = len(inputs)
-    return list(_HipLevelsLoss.apply(config, n, *inputs, *targets))
+    if n == 0:
+        raise ValueError(f"ace_loss_levels takes 1 to {MAX_LEVELS} levels, got 0")
+    x0 = inputs[0]
+    stream = _stream(x0.device) if x0.is_cuda else 0
+    key = (config, stream, x0.get_device(),
+           *[(x.shape, x.dtype, t.shape, t.dtype, t.get_device()) for x, t in zip(inputs, targets)])
+    hit = _LEVEL_CALLS.get(key)
+    if hit is not None and all(x.is_contiguous() for x in inputs) and all(t.is_contiguous() for t in targets):
+        return _lib.autograd().ace_loss_levels(list(inputs), list(targets), hit[0])
+    losses = list(_HipLevelsLoss.apply(config, n, *inputs, *targets))
+    if key not in _LEVEL_CALLS and not capturing(x0.device):
+        plans = [make_plan(x, t, config) for x, t in zip(inputs, targets)]
+        own = all(p.x.data_ptr() == x.data_ptr() and p.x.dtype == x.dtype and x.is_contiguous()
+                  and p.target.data_ptr() == t.data_ptr() and p.target.dtype == t.dtype
+                  and t.is_contiguous() for p, x, t in zip(plans, inputs, targets))
+        if len(_LEVEL_CALLS) >= _MAX_LEVEL_CALLS:
+            _LEVEL_CALLS.clear()
+        _LEVEL_CALLS[key] = _level_signature(plans, config, stream) if own else None
+    return losses

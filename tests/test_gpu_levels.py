@@ -3,7 +3,9 @@ each level's loss and gradient are bit-identical to a separate
 ``ace_loss(..., impl="hip_mi355x")`` call on that level (same blocks, same
 integer sums), for hard and soft binning, every fast channel count,
 background dropped, the three reductions, per-class upstream gradients, an
-empty level, and configurations without a fast kernel rejected."""
+empty level, and configurations without a fast kernel rejected.  Each case
+runs twice: the first call of a levels signature takes the Python autograd
+Function, the second the C++ node (``AceLevelsBackward``)."""
 
 from __future__ import annotations
 
@@ -37,11 +39,20 @@ def _separate(xs, ys, cfg, ups):
     return out
 
 
-def _together(xs, ys, cfg, ups):
+def _together(xs, ys, cfg, ups, node=None):
     leaves = [x.clone().requires_grad_(True) for x in xs]
     losses = ace_loss_levels(leaves, ys, cfg)
+    if node is not None:
+        assert losses[0].grad_fn.name().endswith(node), losses[0].grad_fn.name()
     grads = torch.autograd.grad(losses, leaves, [u.view_as(l) for u, l in zip(ups, losses)])
     return [(l.detach(), g) for l, g in zip(losses, grads)]
+
+
+def _twice(xs, ys, cfg, ups):
+    """The first call (Python Function) and a second one (C++ node)."""
+    first = _together(xs, ys, cfg, ups)
+    second = _together(xs, ys, cfg, ups, node="AceLevelsBackward")
+    return first, second
 
 
 SIZES = [(32, 32, 32), (16, 16, 16), (8, 8, 8), (4, 4, 4)]
@@ -65,10 +76,10 @@ def test_levels_match_separate_calls(binning, c, kw) -> None:
            for _ in SIZES]
     say(f"levels {binning} C={c} {kw}")
     want = _separate(xs, ys, cfg, ups)
-    got = _together(xs, ys, cfg, ups)
-    for (lw, gw), (lg, gg) in zip(want, got):
-        assert torch.equal(lg, lw)
-        assert torch.equal(gg, gw)
+    for got in _twice(xs, ys, cfg, ups):
+        for (lw, gw), (lg, gg) in zip(want, got):
+            assert torch.equal(lg, lw)
+            assert torch.equal(gg, gw)
 
 
 @pytest.mark.parametrize("binning", ["hard", "soft"])
@@ -79,10 +90,28 @@ def test_levels_with_an_empty_level_and_two_levels(binning) -> None:
         ups = [torch.ones(()).cuda() for _ in sizes]
         say(f"levels {binning} {sizes}")
         want = _separate(xs, ys, cfg, ups)
-        got = _together(xs, ys, cfg, ups)
-        for (lw, gw), (lg, gg) in zip(want, got):
-            torch.testing.assert_close(lg, lw, rtol=0, atol=0, equal_nan=True)
-            assert torch.equal(gg, gw)
+        for got in _twice(xs, ys, cfg, ups):
+            for (lw, gw), (lg, gg) in zip(want, got):
+                torch.testing.assert_close(lg, lw, rtol=0, atol=0, equal_nan=True)
+                assert torch.equal(gg, gw)
+
+
+@pytest.mark.parametrize("binning", ["hard", "soft"])
+def test_levels_gradient_of_one_level_only(binning) -> None:
+    """Only the first level's loss reaches the gradient: the other levels'
+    upstream gradients are zero (the node fills them), and inputs that need
+    no gradient get none."""
+    cfg = ACEConfig(binning=binning, to_onehot_y=True, activation="softmax")
+    xs, ys = _levels(2, 4, SIZES[:3], seed=71)
+    ups = [torch.ones(()).cuda() for _ in SIZES[:3]]
+    want0 = _separate(xs[:1], ys[:1], cfg, ups[:1])[0][1]
+    for _ in range(2):
+        leaves = [x.clone().requires_grad_(i != 2) for i, x in enumerate(xs)]
+        losses = ace_loss_levels(leaves, ys, cfg)
+        grads = torch.autograd.grad(losses[0], leaves[:2])
+        assert torch.equal(grads[0], want0)
+        assert not grads[1].any()
+    assert losses[0].grad_fn.name() == "AceLevelsBackward"
 
 
 def test_levels_reject_configurations_without_a_fast_kernel() -> None:
