@@ -182,6 +182,19 @@ def read_ceiling(tensors, steps: int, warmup: int, flush):
             "torch_sum_ms_p50_stream_events": statistics.median(torch_ms)}
 
 
+def copy_ceiling(x, steps: int, warmup: int, flush):
+    """Cold copy of the logits into a same-size buffer (torch's copy kernel:
+    x read once, as many bytes written), timed by events recorded on the
+    stream after the 1 GiB flush: the ceiling beside the backward, which
+    reads the logits and writes as many gradient bytes."""
+    import torch
+
+    out = torch.empty_like(x)
+    ms = statistics.median(time_steps(lambda: out.copy_(x), steps, warmup, flush))
+    nbytes = 2 * x.numel() * x.element_size()
+    return {"bytes": nbytes, "ms_p50_stream_events": ms, "GBps": nbytes / (ms * 1e-3) / 1e9}
+
+
 def host_cost(x, y, cfg, calls: int = 200):
     """Host microseconds per call, each call issued to an idle device
     (synchronised before, not after: the time is the host's alone); median
@@ -267,9 +280,11 @@ def bench_workload(wl, steps: int, warmup: int, flush):
                                  flush)
     # the same launches timed by events recorded on the stream around them
     fwd_stream = time_steps(lambda: hip.hip_forward(pl, cfg), steps, warmup, flush)
+    bwd_stream = time_steps(lambda: hip.hip_backward(pl, coef, d, jac, go), steps, warmup, flush)
     fwd_ms = statistics.fmean(fwd_cold)
     bwd_ms = statistics.fmean(bwd_cold)
     ceiling = read_ceiling((x.detach(), y), steps, warmup, flush)
+    copy = copy_ceiling(x.detach(), steps, warmup, flush)
     host = host_cost(x, y, cfg)
     b2b = time_back_to_back(step, 50, 5)
 
@@ -290,11 +305,17 @@ def bench_workload(wl, steps: int, warmup: int, flush):
         "fwd_ms": _quantiles(fwd_cold),
         "bwd_ms": _quantiles(bwd_cold),
         "fwd_ms_stream_events": _quantiles(fwd_stream),
+        "bwd_ms_stream_events": _quantiles(bwd_stream),
         "fwd_GBps": wl.ideal_bytes("fwd") / (statistics.median(fwd_cold) * 1e-3) / 1e9,
         "graph_replay_matches_eager": graph_ok,
         "loss": float(loss.item()),
         "read_ceiling": ceiling,
         "fwd_frac_of_read_ceiling": (ceiling["ms_p50"] / statistics.median(fwd_cold)),
+        # both timed by events on the stream (the backward of a problem
+        # above 224 MB writes its gradient with nontemporal stores, so its
+        # bytes reach HBM inside the kernel; the copy's stay in the cache)
+        "copy_ceiling": copy,
+        "bwd_frac_of_copy_ceiling": copy["ms_p50_stream_events"] / statistics.median(bwd_stream),
         "host_us": host,
         "back_to_back_ms": b2b,
     }
@@ -593,9 +614,15 @@ def live_traffic(idx: int, kernel: str):
 COPY_KIB = 262144.0  # profile_kernels' calibration copy: 256 MiB read and 256 MiB written
 
 
+_KERNEL_DTYPES = {"float": "torch.float32", "__hip_bfloat16": "torch.bfloat16", "_Float16": "torch.float16",
+                  "__half": "torch.float16"}
+
+
 def _profile_key(name: str, workloads):
     """(kernel, workload index) of a dispatch in a ``--profile-kernels`` run
-    over ``workloads`` (one hard, one soft workload), or ("copy", None)."""
+    over ``workloads``, or ("copy", None): the first workload whose binning,
+    logit dtype and, for the fast kernels, channel count and background flag
+    match the kernel's template arguments."""
     if "copyBuffer" in name:
         return "copy", None
     if "ace::" not in name or "levels" in name:
@@ -604,13 +631,20 @@ def _profile_key(name: str, workloads):
     if kernel is None:
         return None
     args = [a.strip() for a in name[name.index("<") + 1:name.index(">")].split(",")]
-    # fast kernels: <T, C, VEC, SOFT, RIGHT, SKIP0>; generic: <T, CMAX, EXACT, VEC, SOFT, RIGHT>
-    soft = args[3] == "true" if "_fast" in name else args[4] == "true"
+    # fast kernels: <T, C, VEC, SOFT, RIGHT, SKIP0[, STREAM]>; generic: <T, CMAX, EXACT, VEC, SOFT, RIGHT>
+    fast = "_fast" in name
+    soft = args[3] == "true" if fast else args[4] == "true"
+    dtype = _KERNEL_DTYPES.get(args[0])
     from ace_kernels.workloads import workload
 
     for idx in workloads:
-        if (workload(idx).config.binning == "soft") == soft:
-            return kernel, idx
+        wl = workload(idx)
+        if (wl.config.binning == "soft") != soft or (dtype is not None and str(wl.dtype) != dtype):
+            continue
+        if fast and (int(args[1]) != wl.channels
+                     or (args[5] == "true") != (not wl.config.include_background)):
+            continue
+        return kernel, idx
     return None
 
 
@@ -859,6 +893,7 @@ def main() -> int:
             "read_ceiling_frac": main_r["read_ceiling"]["frac_of_peak"],
         },
         "fwd_frac_of_read_ceiling": main_r["fwd_frac_of_read_ceiling"],
+        "bwd_frac_of_copy_ceiling": main_r["bwd_frac_of_copy_ceiling"],
         "host_us": main_r["host_us"],
         "back_to_back_ms": main_r["back_to_back_ms"],
         "workloads": results,
