@@ -233,7 +233,7 @@ def host_cost(x, y, cfg, calls: int = 200):
     return out
 
 
-def bench_workload(wl, steps: int, warmup: int, flush):
+def bench_workload(wl, steps: int, warmup: int, flush, host: bool = True):
     import torch
 
     from ace_kernels import ace_loss
@@ -285,8 +285,8 @@ def bench_workload(wl, steps: int, warmup: int, flush):
     bwd_ms = statistics.fmean(bwd_cold)
     ceiling = read_ceiling((x.detach(), y), steps, warmup, flush)
     copy = copy_ceiling(x.detach(), steps, warmup, flush)
-    host = host_cost(x, y, cfg)
-    b2b = time_back_to_back(step, 50, 5)
+    host_us = host_cost(x, y, cfg) if host else None
+    b2b = time_back_to_back(step, 50, 5) if host else None
 
     n_vox = wl.batch * wl.voxels
     xb = wl.input_bytes()
@@ -316,7 +316,7 @@ def bench_workload(wl, steps: int, warmup: int, flush):
         # bytes reach HBM inside the kernel; the copy's stay in the cache)
         "copy_ceiling": copy,
         "bwd_frac_of_copy_ceiling": copy["ms_p50_stream_events"] / statistics.median(bwd_stream),
-        "host_us": host,
+        "host_us": host_us,
         "back_to_back_ms": b2b,
     }
     p50 = out["eager_ms"]["p50"]
@@ -788,6 +788,9 @@ def main() -> int:
     ap.add_argument("--no-deepsup", action="store_true", help="skip the deep-supervision steps")
     ap.add_argument("--no-counters", action="store_true",
                     help="no live rocprofv3 traffic runs (for runs under a profiler)")
+    ap.add_argument("--no-host", action="store_true",
+                    help="skip the host-cost and back-to-back timings, whose launches run warm "
+                         "(for kernel traces whose averages should be the cold launches')")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="LAUNCHES",
                     help="only launch the kernels LAUNCHES times each (for rocprofv3)")
     ap.add_argument("--timeline", type=int, default=0, metavar="LAUNCHES",
@@ -821,7 +824,7 @@ def main() -> int:
     for idx in [int(v) for v in args.workloads.split(",")]:
         wl = workload(idx)
         log(f"bench {wl.name}: steps={args.steps} warmup={args.warmup}")
-        results.append(bench_workload(wl, args.steps, args.warmup, flush))
+        results.append(bench_workload(wl, args.steps, args.warmup, flush, host=not args.no_host))
         log(json.dumps(results[-1]))
     deepsup = []
     if not args.no_deepsup:
