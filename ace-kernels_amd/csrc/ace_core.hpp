@@ -1164,8 +1164,10 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
   const int rows = P.B * CL;
   if (P.epi_all) {
     const float total = epilogue<SOFT, MOM>(P, hist, repl, CK, CL, 0, P.B);
+    fast_stamp(P, kTlEpiEnd);
     if (tid == 0 && P.red != kRedNone)
       P.loss[0] = P.red == kRedMean ? total / (float)rows : total;
+    fast_stamp(P, kTlLoss);
     return;
   }
   // ---- loss.  The loss ticket is drawn as b's epilogue starts, so that its
