@@ -304,19 +304,23 @@ def hip_ace(input: torch.Tensor, target: torch.Tensor, config: ACEConfig) -> tor
     A remembered signature runs in C++ (``_Call``); any other call builds a
     ``Plan`` and runs the autograd Function above (or, with no gradient to
     record, the forward alone), and remembers its signature once it has
-    succeeded."""
+    succeeded.  The target gets no gradient (None), as in the reference's
+    ``_V6Loss.backward`` (``impls/v6_triton.py:107-111``)."""
     stream = _stream(input.device) if input.is_cuda else 0
     key = (config, input.shape, input.dtype, target.shape, target.dtype, input.get_device(),
            target.get_device(), stream)
     call = _CALLS.get(key)
-    if call is not None and input.is_contiguous() and target.is_contiguous():
+    # a target that needs a gradient (and gets none, as in the reference's
+    # autograd Function) takes the Function below, so that the loss records
+    # autograd history even when the input needs no gradient
+    if call is not None and not target.requires_grad and input.is_contiguous() and target.is_contiguous():
         loss: torch.Tensor = _lib.autograd().ace_loss(input, target, call.sig)
         return loss
     pl = make_plan(input, target, config)
     own = (pl.x.data_ptr() == input.data_ptr() and pl.x.dtype == input.dtype and input.is_contiguous()
            and pl.target.data_ptr() == target.data_ptr() and pl.target.dtype == target.dtype
            and target.is_contiguous())
-    if torch.is_grad_enabled() and input.requires_grad:
+    if torch.is_grad_enabled() and (input.requires_grad or target.requires_grad):
         loss = _HipACELoss.apply(input, target, config, pl)
     else:
         loss = hip_forward(pl, config)[0]

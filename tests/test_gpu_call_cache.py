@@ -168,3 +168,28 @@ def test_upstream_gradient_through_the_node() -> None:
             out = ace_loss(leaf, y, cfg, impl="hip_mi355x")
             (3.0 * out).sum().backward()
             assert torch.equal(leaf.grad, want)
+
+
+def test_target_that_needs_a_gradient_gets_none() -> None:
+    """A float one-hot target that requires grad: the loss records autograd
+    history even when the input needs no gradient, and the target's gradient
+    is None, as from the reference's autograd Function
+    (``impls/v6_triton.py:107-111``); with an input that needs one, the
+    input's gradient is the usual one."""
+    cfg = ACEConfig(binning="soft", num_bins=20, to_onehot_y=False)
+    gen = torch.Generator().manual_seed(21)
+    x = (torch.randn((2, 4, 9, 33), generator=gen) * 2).cuda()
+    lab = torch.randint(0, 4, (2, 9, 33), generator=gen)
+    y = torch.nn.functional.one_hot(lab, 4).permute(0, 3, 1, 2).float().cuda()
+    want = _general(x, y, cfg)[1]
+    for _ in range(3):  # the signature is remembered after the first call
+        t = y.clone().requires_grad_(True)
+        loss = ace_loss(x, t, cfg, impl="hip_mi355x")
+        assert loss.requires_grad
+        loss.backward()
+        assert t.grad is None
+        leaf = x.clone().requires_grad_(True)
+        t = y.clone().requires_grad_(True)
+        loss = ace_loss(leaf, t, cfg, impl="hip_mi355x")
+        loss.backward()
+        assert t.grad is None and torch.equal(leaf.grad, want)
