@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("ACE_HIP_LIB", Path(__file__).resolve().with_name("libace_hip.so")))
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # enums of include/ace_hip.h
 F32, BF16, F16, F64 = 0, 1, 2, 3
@@ -35,6 +35,7 @@ EXPORTS = (
     "ace_set_test_hooks",
     "ace_read_bytes_scratch",
     "ace_read_bytes",
+    "ace_probabilities",
     "ace_set_timeline",
     "ace_workspace_bytes_levels",
     "ace_forward_levels",
@@ -46,7 +47,7 @@ EXPORTS = (
 
 # ace_forward_noalloc's scratch (ACE_NOALLOC_SCRATCH_BYTES) and its error code
 NOALLOC_SCRATCH_BYTES = 1 << 20
-ESCRATCH = 4
+EINVAL, EUNSUPPORTED, ESCRATCH = 1, 2, 4
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -169,6 +170,8 @@ def lib() -> ctypes.CDLL:
     handle.ace_read_bytes_scratch.argtypes = []
     handle.ace_read_bytes.restype = _i
     handle.ace_read_bytes.argtypes = [_p, _sz, _p, _sz, _p, _p]
+    handle.ace_probabilities.restype = _i
+    handle.ace_probabilities.argtypes = [_p, _i, _i64, _i64, _i64, _i, _p, _p]
     handle.ace_set_timeline.restype = _i
     handle.ace_set_timeline.argtypes = [_p]
     version = handle.ace_abi_version()

@@ -118,6 +118,27 @@ def _stream(dev: torch.device) -> int:
     return torch._C._cuda_getCurrentRawStream(index)
 
 
+def _d_values(pl: Plan) -> int:
+    """Values of the forward's d: soft float32 outputs hold d rounded to
+    float32 and its remainder ([2, B, C', K], the backward adds both);
+    otherwise [B, C', K]."""
+    bck = pl.B * pl.CL * pl.K
+    return 2 * bck if pl.soft and pl.dtype_code != _lib.F64 else bck
+
+
+def _d_shape(pl: Plan) -> Tuple[int, ...]:
+    per = (pl.B, pl.CL, pl.K)
+    return (2, *per) if _d_values(pl) > pl.B * pl.CL * pl.K else per
+
+
+def saved_layout(pl: Plan, reduced: bool) -> Tuple[int, int, int, int]:
+    """(values, d's byte offset, jac's, the per-class errors') of the one
+    float32 allocation of a C++ loss call: coef, d, jac, then the per-class
+    errors unless they are the returned loss."""
+    bck, bc, nd = pl.B * pl.CL * pl.K, pl.B * pl.CL, _d_values(pl)
+    return bck + nd + bc + (bc if reduced else 0), 4 * bck, 4 * (bck + nd), 4 * (bck + nd + bc)
+
+
 @lru_cache(maxsize=256)
 def _workspace_bytes(dims: Tuple[int, ...]) -> int:
     return _lib.lib().ace_workspace_bytes(*dims)
@@ -125,6 +146,8 @@ def _workspace_bytes(dims: Tuple[int, ...]) -> int:
 
 def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False, shared: bool = True):
     """(loss, coef, d, jac, per_class, stats-or-None) via ``ace_forward``.
+    d is [B, C', K], or for soft binning in float32 [2, B, C', K]: d rounded
+    to float32 (``d[0]``) and its remainder (``d[1]``).
     ``shared``: coef, d and jac are views of one allocation (one allocator
     call instead of three); the custom op, whose outputs may not alias,
     passes False."""
@@ -139,15 +162,15 @@ def hip_forward(pl: Plan, config: ACEConfig, stats: bool = False, shared: bool =
     # coef, d and jac (all saved for backward) share one allocation; the
     # per-class errors and the loss, which the caller may receive and modify
     # in place, have their own
-    bck, bc = pl.B * pl.CL * pl.K, pl.B * pl.CL
+    bck, bc, nd = pl.B * pl.CL * pl.K, pl.B * pl.CL, _d_values(pl)
     if shared:
-        saved = torch.empty(2 * bck + bc, dtype=out_dtype, device=dev)
+        saved = torch.empty(bck + nd + bc, dtype=out_dtype, device=dev)
         coef = saved[:bck].view(pl.B, pl.CL, pl.K)
-        d = saved[bck:2 * bck].view(pl.B, pl.CL, pl.K)
-        jac = saved[2 * bck:].view(pl.B, pl.CL)
+        d = saved[bck:bck + nd].view(_d_shape(pl))
+        jac = saved[bck + nd:].view(pl.B, pl.CL)
     else:
         coef = torch.empty((pl.B, pl.CL, pl.K), dtype=out_dtype, device=dev)
-        d = torch.empty_like(coef)
+        d = torch.empty(_d_shape(pl), dtype=out_dtype, device=dev)
         jac = torch.empty((pl.B, pl.CL), dtype=out_dtype, device=dev)
     per_class = torch.empty((pl.B, pl.CL), dtype=out_dtype, device=dev)
     reduction = _REDUCTIONS[config.reduction]
@@ -198,6 +221,11 @@ def hip_backward(pl: Plan, coef: torch.Tensor, d: torch.Tensor, jac: torch.Tenso
     if not go.is_contiguous():
         go = go.contiguous()
     dx = torch.empty_like(pl.x)
+    if pl.soft and not f64 and d.dim() == 3:
+        # a float32 d without its remainder (not this forward's output)
+        d = torch.cat([d.reshape(-1).float(), d.new_zeros(d.numel(), dtype=torch.float32)])
+    if d.numel() != _d_values(pl) or not d.is_contiguous():
+        raise ValueError(f"d must be the forward's contiguous {_d_shape(pl)} output, got {tuple(d.shape)}")
     if f64:
         rc = lib.ace_backward_f64(
             pl.x.data_ptr(), pl.target.data_ptr() if pl.soft else None, pl.target_kind,
@@ -253,7 +281,6 @@ def _build_call(pl: Plan, config: ACEConfig, stream: int) -> Optional[_Call]:
     ws = workspace(dev, stream, _workspace_bytes(dims))
     weights = class_weights(config, pl.CL)
     cw = class_weight_tensor(tuple(weights), dev) if weights is not None else None
-    bck, bc = pl.B * pl.CL * pl.K, pl.B * pl.CL
     reduction = _REDUCTIONS[config.reduction]
     reduced = reduction != _lib.RED_NONE
     c = _Call()
@@ -261,7 +288,7 @@ def _build_call(pl: Plan, config: ACEConfig, stream: int) -> Optional[_Call]:
         pl.dtype_code, pl.target_kind, pl.B, pl.C, pl.N, pl.K, binning, pl.act, int(pl.include_bg),
         int(config.ignore_empty_classes), reduction, int(pl.right), float(config.empty_weight),
         _ptr(cw) or 0, pl.btab.data_ptr(), _ptr(pl.rtab) or 0, ws.data_ptr(), ws.numel(),
-        2 * bck + bc + (bc if reduced else 0), 4 * bck, 8 * bck, 4 * (2 * bck + bc), reduced, pl.soft,
+        *saved_layout(pl, reduced), reduced, pl.soft,
         [] if reduced else [pl.B, pl.CL, *([1] * pl.spatial_ndim)])
     c.ws, c.tables = ws, (cw, pl.btab, pl.rtab)  # kept alive with the signature
     return c
@@ -383,7 +410,9 @@ def _(input: torch.Tensor, target: torch.Tensor, config_json: str) -> Outputs:
     loss_shape = (b, cl, *([1] * (input.dim() - 2))) if config.reduction == "none" else ()
     loss = input.new_empty(loss_shape, dtype=out)
     jac = input.new_empty((b, cl), dtype=out)
-    return loss, per_bin, torch.empty_like(per_bin), jac
+    # soft float32: d and its remainder
+    d_shape = (2, b, cl, config.num_bins) if config.binning == "soft" and out == torch.float32 else per_bin.shape
+    return loss, per_bin, input.new_empty(d_shape, dtype=out), jac
 
 
 @torch.library.custom_op("ace_kernels::hip_backward", mutates_args=())

@@ -30,7 +30,7 @@ import torch
 from ace_kernels import _lib
 from ace_kernels.common import capturing, class_weight_tensor, class_weights, workspace
 from ace_kernels.config import ACEConfig
-from ace_kernels.impls.hip_mi355x import Plan, _ptr, _stream, make_plan
+from ace_kernels.impls.hip_mi355x import Plan, _d_shape, _d_values, _ptr, _stream, make_plan, saved_layout
 
 _REDUCTIONS = {"mean": _lib.RED_MEAN, "sum": _lib.RED_SUM, "none": _lib.RED_NONE}
 MAX_LEVELS = 4
@@ -65,14 +65,15 @@ def forward_levels(plans: Sequence[Plan], config: ACEConfig):
     reduction = _REDUCTIONS[config.reduction]
     f32 = torch.float32
     bck, bc = p0.B * p0.CL * p0.K, p0.B * p0.CL
+    nd = _d_values(p0)
     outs = []
     keep = []  # buffers the launch writes that the caller does not get back
     arr = (_lib.AceFwdLevel * n)()
     for i, p in enumerate(plans):
-        saved = torch.empty(2 * bck + bc, dtype=f32, device=dev)
+        saved = torch.empty(bck + nd + bc, dtype=f32, device=dev)
         coef = saved[:bck].view(p.B, p.CL, p.K)
-        d = saved[bck:2 * bck].view(p.B, p.CL, p.K)
-        jac = saved[2 * bck:].view(p.B, p.CL)
+        d = saved[bck:bck + nd].view(_d_shape(p))
+        jac = saved[bck + nd:].view(p.B, p.CL)
         per_class = torch.empty((p.B, p.CL), dtype=f32, device=dev)
         keep.append(per_class)
         loss = torch.empty((), dtype=f32, device=dev) if reduction != _lib.RED_NONE else None
@@ -167,12 +168,11 @@ def _level_signature(plans: Sequence[Plan], config: ACEConfig, stream: int):
     cw = class_weight_tensor(tuple(weights), dev) if weights is not None else None
     reduction = _REDUCTIONS[config.reduction]
     reduced = reduction != _lib.RED_NONE
-    bck, bc = p0.B * p0.CL * p0.K, p0.B * p0.CL
     sig = _lib.autograd().make_level_signature(
         p0.dtype_code, p0.B, p0.C, p0.K, binning, int(p0.include_bg), int(config.ignore_empty_classes),
         reduction, int(p0.right), float(config.empty_weight), _ptr(cw) or 0, p0.btab.data_ptr(),
         _ptr(p0.rtab) or 0, ws.data_ptr(), ws.numel(), [p.N for p in plans],
-        2 * bck + bc + (bc if reduced else 0), 4 * bck, 8 * bck, 4 * (2 * bck + bc), reduced, p0.soft,
+        *saved_layout(p0, reduced), reduced, p0.soft,
         [] if reduced else [p0.B, p0.CL, *([1] * p0.spatial_ndim)])
     return sig, (ws, cw, p0.btab, p0.rtab)
 

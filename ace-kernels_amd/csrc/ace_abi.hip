@@ -425,6 +425,24 @@ __global__ void __launch_bounds__(kFastThreads) read_bytes_kernel(const uint4* a
   if (acc == 0x2545f491u) out[blockIdx.x] = acc;
 }
 
+// ace_probabilities: activate (the activation of every forward and backward
+// kernel) of one voxel per lane, written as float32.
+template <typename T>
+__global__ void __launch_bounds__(kThreads) probabilities_kernel(const T* x, int64_t batch, int nc,
+                                                                 int64_t n, int act, float* p) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= batch * n) return;
+  const int64_t b = i / n;
+  const int64_t off = b * nc * n + (i - b * n);
+  float v[kMaxChannels];
+#pragma unroll
+  for (int c = 0; c < kMaxChannels; ++c) v[c] = c < nc ? to_f32<T>(x[off + c * n]) : 0.0f;
+  activate<kMaxChannels, false>(v, nc, act);
+#pragma unroll
+  for (int c = 0; c < kMaxChannels; ++c)
+    if (c < nc) p[off + c * n] = v[c];
+}
+
 }  // namespace
 }  // namespace ace
 
@@ -440,7 +458,7 @@ using namespace ace;
 
 extern "C" {
 
-int ace_abi_version(void) { return 8; }
+int ace_abi_version(void) { return 9; }
 
 const char* ace_error_string(int code) {
   switch (code) {
@@ -729,6 +747,37 @@ int ace_read_bytes(const void* a, size_t a_bytes, const void* b, size_t b_bytes,
                                       ev.stop, 0));
   }
   hipLaunchKernelGGL(read_bytes_kernel, dim3(kReadBlocks), dim3(kFastThreads), 0, s, pa, na, pb, nb, out);
+  return to_code(hipGetLastError());
+}
+
+int ace_probabilities(const void* x, int x_dtype, int64_t batch, int64_t channels, int64_t voxels,
+                      int activation, float* p, void* stream) {
+  if (batch < 0 || channels < 1 || voxels < 0) return ACE_EINVAL;
+  if (activation < kActNone || activation > kActSigmoid) return ACE_EINVAL;
+  if (channels > kMaxChannels) return ACE_EUNSUPPORTED;
+  const int64_t n = batch * voxels;
+  if (n == 0) return ACE_OK;
+  if (!x || !p) return ACE_EINVAL;
+  if ((n + kThreads - 1) / kThreads > INT32_MAX) return ACE_EUNSUPPORTED;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
+  const int nc = (int)channels;
+  switch (x_dtype) {
+    case ACE_F32:
+      hipLaunchKernelGGL(probabilities_kernel<float>, grid, dim3(kThreads), 0, s,
+                         static_cast<const float*>(x), batch, nc, voxels, activation, p);
+      break;
+    case ACE_BF16:
+      hipLaunchKernelGGL(probabilities_kernel<__hip_bfloat16>, grid, dim3(kThreads), 0, s,
+                         static_cast<const __hip_bfloat16*>(x), batch, nc, voxels, activation, p);
+      break;
+    case ACE_F16:
+      hipLaunchKernelGGL(probabilities_kernel<__half>, grid, dim3(kThreads), 0, s,
+                         static_cast<const __half*>(x), batch, nc, voxels, activation, p);
+      break;
+    default:
+      return ACE_EINVAL;
+  }
   return to_code(hipGetLastError());
 }
 

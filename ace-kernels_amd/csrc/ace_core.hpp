@@ -376,16 +376,41 @@ __device__ __forceinline__ SoftW soft_assign(float p, int K, float n2f, const fl
   return w;
 }
 
+// The same assignment with the exact-arithmetic weights of the moments
+// kernels: ld, rd and S formed in float64 from the float32 p and centres,
+// lw = rd / S and rw = ld / S rounded once in float64, where the float32 form
+// rounds ld, rd, S and both quotients (each ~1e-7 relative).  The generic
+// soft forward sums these: the soft gradient takes d = P/W - G/W amplified
+// by 2K / W, and float32 weights move d by ~1e-7 there.
+struct SoftW64 {
+  int l, r;
+  double lw, rw;
+};
+template <bool RIGHT>
+__device__ __forceinline__ SoftW64 soft_assign64(float p, int K, float n2f, const float* htab,
+                                                 const float* repl) {
+  const int n2 = 2 * K;
+  const int h = bucket<RIGHT>(p, n2f, n2, htab);
+  SoftW64 w;
+  w.l = max(h - 1, 0) >> 1;
+  w.r = min(h + 1, n2 - 1) >> 1;
+  const double ld = (double)p - (double)repl[h];
+  const double rd = (double)repl[h + 2] - (double)p;
+  const double inv = 1.0 / (ld + rd);
+  w.lw = rd * inv;
+  w.rw = ld * inv;
+  return w;
+}
+
 // Fixed-point value of a float32 term with |v| < 2 (2^30 scale, rounded to
 // nearest even): exact for |v| >= 2^-7.
 __device__ __forceinline__ long long fx(float v) {
   return (long long)(int)rintf(v * 1073741824.0f);
 }
-// The same at scale sfx = 2^f (soft_frac: up to 2^40), exact for
-// |v| >= 2^(23 - f): v sfx is exact in float32 and below 2^41, so it is
-// converted through float64.
-__device__ __forceinline__ long long fx_soft(float v, float sfx) {
-  return (long long)__builtin_rint((double)(v * sfx));
+// A float64 term |v| < 2 at scale sfx = 2^f (soft_frac: up to 2^40), rounded
+// to nearest: an error of at most 2^-(f+1) per term.
+__device__ __forceinline__ long long fx_soft(double v, float sfx) {
+  return (long long)__builtin_rint(v * (double)sfx);
 }
 
 __device__ __forceinline__ void lds_add(unsigned long long* p, unsigned long long v) {
@@ -575,17 +600,17 @@ __device__ __forceinline__ void fwd_accumulate(const FwdParams& P, const Hist& H
       }
     } else {
       int gl = 0, gr = 0;
-      float glw = 0.0f, grw = 0.0f;
+      double glw = 0.0, grw = 0.0;
 #pragma unroll
       for (int c = 0; c < CMAX; ++c) {
         if (!(EXACT || c < nc) || c < off) continue;
-        const SoftW w = soft_assign<RIGHT>(p[c], K, nf, btab, repl);
+        const SoftW64 w = soft_assign64<RIGHT>(p[c], K, nf, btab, repl);
         const int sl = ((c - off) * K + w.l) * R + copy;
         const int sr = ((c - off) * K + w.r) * R + copy;
         lds_add(&H.w[sl], fx_soft(w.lw, P.sfx));
         lds_add(&H.w[sr], fx_soft(w.rw, P.sfx));
-        lds_add(&H.p[sl], fx_soft(w.lw * p[c], P.sfx));
-        lds_add(&H.p[sr], fx_soft(w.rw * p[c], P.sfx));
+        lds_add(&H.p[sl], fx_soft(w.lw * (double)p[c], P.sfx));
+        lds_add(&H.p[sr], fx_soft(w.rw * (double)p[c], P.sfx));
         if (labels) {
           const bool hit = lab[j] == c;
           gl = hit ? sl : gl;
@@ -595,8 +620,8 @@ __device__ __forceinline__ void fwd_accumulate(const FwdParams& P, const Hist& H
         } else {
           const float y = yv[c][j];
           if (y != 0.0f) {
-            lds_add(&H.g[sl], fx_soft(w.lw * y, P.sfx));
-            lds_add(&H.g[sr], fx_soft(w.rw * y, P.sfx));
+            lds_add(&H.g[sl], fx_soft(w.lw * (double)y, P.sfx));
+            lds_add(&H.g[sr], fx_soft(w.rw * (double)y, P.sfx));
           }
         }
       }
@@ -819,21 +844,31 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
     const float Pf = (float)Pd;
     const float Gf = (float)Gd;
     const bool empty = SOFT ? !(Wf >= P.empty_w) : (Wf == 0.0f);
-    // d = P/W - G/W in the reference's float32 order (binning.py:136-141):
-    // two quotients rounded to float32, then their difference.  Soft binning
-    // forms the quotients from the float64 sums (one rounding each instead of
-    // rounding the sums first): the soft gradient takes d amplified by
-    // 2K / W through (p - y - d) / S, and in a bin of one voxel the moments'
-    // quotients are then exactly (the quantised) p and y, so d = fl(p - y)
-    // cancels the backward's float32 residual fl(p - y), as in the reference.
-    float dd = 0.0f;
-    if (!empty)
-      dd = SOFT ? (float)(Pd / Wd) - (float)(Gd / Wd) : Pf / Wf - Gf / Wf;
+    // d = P/W - G/W (binning.py:136-141).  Hard: the reference's float32
+    // order, two quotients rounded to float32, then their difference.  Soft:
+    // (P - G) / W from the float64 sums, stored as its float32 rounding and
+    // the remainder (diff[0] and diff[1]).  The soft gradient takes d
+    // amplified by 2K / W through (p - y - d) / S, where a float32 d (a few
+    // 1e-8 off wherever P/W and G/W nearly cancel) moves dL/dp by ~1e-7; the
+    // backward adds both parts, so p - y - d keeps the precision of the sums,
+    // and in a bin of one voxel (d = p - y exactly) it cancels to 0.  The loss
+    // and sign(d) take the rounded value.
+    float dd = 0.0f, dlo = 0.0f;
+    if (!empty) {
+      if constexpr (SOFT) {
+        const double dx = (Pd - Gd) / Wd;
+        dd = (float)dx;
+        dlo = (float)(dx - (double)dd);
+      } else {
+        dd = Pf / Wf - Gf / Wf;
+      }
+    }
     sd[i] = dd;
     sw[i] = Wf;
     sg[i] = Gf;
     se[i] = empty ? 1 : 0;
     P.d[o] = dd;
+    if constexpr (SOFT) P.d[BCK + o] = dlo;
   };
   if constexpr (MOM) {
     const long long none[3] = {0, 0, 0};
@@ -1312,8 +1347,9 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
 // dL/dx of NV voxels, in place in xv (logits in, gradient out).
 template <int CMAX, bool EXACT, int NV, bool SOFT, bool RIGHT>
 __device__ __forceinline__ void bwd_voxels(const BwdParams& P, const float* btab, const float* repl,
-                                           const float* scoef, const float* sdd, const float* sg,
-                                           int nc, float (&xv)[CMAX][NV], const int (&lab)[NV],
+                                           const float* scoef, const float* sdd, const float* sdl,
+                                           const float* sg, int nc, float (&xv)[CMAX][NV],
+                                           const int (&lab)[NV],
                                            const float (&yv)[CMAX][NV], bool labels) {
   const int K = P.K;
   const int off = P.off;
@@ -1336,9 +1372,17 @@ __device__ __forceinline__ void bwd_voxels(const BwdParams& P, const float* btab
       } else {
         const SoftW w = soft_assign<RIGHT>(p[c], K, nf, btab, repl);
         const float y = labels ? (lab[j] == c ? 1.0f : 0.0f) : yv[c][j];
-        const float resid = p[c] - y;
-        const float left = scoef[cl * K + w.l] * (w.lw - w.inv_span * (resid - sdd[cl * K + w.l]));
-        const float rght = scoef[cl * K + w.r] * (w.rw + w.inv_span * (resid - sdd[cl * K + w.r]));
+        // p - y - d (v2_autograd.py:94-104) with p - y = s + e exactly
+        // (TwoSum) and d = d_hi + d_lo: (s - d_hi) + (e - d_lo), so that the
+        // residual carries neither the float32 rounding of p - y nor that of d
+        const float s = p[c] - y;
+        const float sp = s - p[c];
+        const float e = (p[c] - (s - sp)) + (-y - sp);
+        const int il = cl * K + w.l, ir = cl * K + w.r;
+        const float rl = (s - sdd[il]) + (e - sdl[il]);
+        const float rr = (s - sdd[ir]) + (e - sdl[ir]);
+        const float left = scoef[il] * (w.lw - w.inv_span * rl);
+        const float rght = scoef[ir] * (w.rw + w.inv_span * rr);
         gp[c] = sg[cl] * (left + rght);
       }
     }
@@ -1393,12 +1437,17 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
 
   const size_t tab_floats = (size_t)(((n + 2) + (SOFT ? 2 * K + 2 : 0) + 3) / 4 * 4);
   float* scoef = tabs + tab_floats;
-  float* sdd = scoef + CK;
-  float* sg = sdd + (SOFT ? CK : 0);
+  float* sdd = scoef + CK;          // soft: d rounded to float32 (diff[0])
+  float* sdl = sdd + CK;            // soft: its remainder (diff[1])
+  float* sg = sdd + (SOFT ? 2 * CK : 0);
   load_tables(tabs, P.btab, P.rtab, n, SOFT ? 2 * K + 2 : 0);
+  const int64_t BCK = (int64_t)P.B * CK;
   for (int t = tid; t < CK; t += kThreads) {
     scoef[t] = P.coef[(int64_t)b * CK + t];
-    if (SOFT) sdd[t] = P.d[(int64_t)b * CK + t];
+    if (SOFT) {
+      sdd[t] = P.d[(int64_t)b * CK + t];
+      sdl[t] = P.d[BCK + (int64_t)b * CK + t];
+    }
   }
   for (int t = tid; t < CL; t += kThreads) {
     const float go = P.go_per_class ? P.go[b * CL + t] : P.go[0];
@@ -1428,14 +1477,14 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
     for (; v < nfull; v += 2 * stride) {
       if (v + stride < nfull)
         bwd_load<T, EXACT, CMAX, VEC>(tb, xt, lt, yt, N, v + stride, nc, off, labels, need_tgt);
-      bwd_voxels<CMAX, EXACT, VEC, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sg, nc, ta.x, ta.lab, ta.y, labels);
+      bwd_voxels<CMAX, EXACT, VEC, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sdl, sg, nc, ta.x, ta.lab, ta.y, labels);
 #pragma unroll
       for (int c = 0; c < CMAX; ++c)
         if (EXACT || c < nc) store_vec<T, VEC>(dt + c * N + v, ta.x[c]);
       if (v + 2 * stride < nfull)
         bwd_load<T, EXACT, CMAX, VEC>(ta, xt, lt, yt, N, v + 2 * stride, nc, off, labels, need_tgt);
       if (v + stride < nfull) {
-        bwd_voxels<CMAX, EXACT, VEC, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sg, nc, tb.x, tb.lab, tb.y, labels);
+        bwd_voxels<CMAX, EXACT, VEC, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sdl, sg, nc, tb.x, tb.lab, tb.y, labels);
 #pragma unroll
         for (int c = 0; c < CMAX; ++c)
           if (EXACT || c < nc) store_vec<T, VEC>(dt + c * N + v + stride, tb.x[c]);
@@ -1458,7 +1507,7 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
           if ((EXACT || c < nc) && c >= off) load_row<float, 1>(yt + c * N + v, yv[c]);
       }
     }
-    bwd_voxels<CMAX, EXACT, 1, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sg, nc, xv, lab, yv, labels);
+    bwd_voxels<CMAX, EXACT, 1, SOFT, RIGHT>(P, btab, repl, scoef, sdd, sdl, sg, nc, xv, lab, yv, labels);
 #pragma unroll
     for (int c = 0; c < CMAX; ++c)
       if (EXACT || c < nc) dt[c * N + v] = from_f32<T>(xv[c][0]);
@@ -1942,15 +1991,17 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
 // the order of 2K coef g, while dL/dp is a small residual wherever p - y - d
 // is small (bins of a few well-calibrated voxels), so the form is evaluated
 // from the half-bin's lower boundary e instead: A_y + B (p - e) with
-// A_y = A + B (e - y/2) formed in float64 for y = 0 and y = 1.  p - e is
+// A_y = A + B (e - y/2) formed in float64 for y = 0 and y = 1, from
+// d = d_hi + d_lo (sdd, sdl: the float64 d of the forward's sums).  p - e is
 // exact in float32 (e <= p <= 2e for h >= 1, Sterbenz; e = 0 for h = 0) and
 // at most 1/(2K), so no float32 term is larger than dL/dp by more than ~2
-// coef g.  sab[4h .. 4h + 3] = (A_0, A_1, B, e) for half-bin h of every loss
+// coef g, and each voxel's dL/dp takes two roundings (A_y's and the fma's).
+// sab[4h .. 4h + 3] = (A_0, A_1, B, e) for half-bin h of every loss
 // channel; tab is the padded half-boundary table (tab[h] = e for h >= 1).
 __device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const float* tab,
                                                            const float* repl, const float* scoef,
-                                                           const float* sdd, const float* sg,
-                                                           int K, int CL) {
+                                                           const float* sdd, const float* sdl,
+                                                           const float* sg, int K, int CL) {
   const int H = 2 * K;
   for (int t = threadIdx.x; t < CL * H; t += kThreads) {
     const int cl = t / H;
@@ -1960,7 +2011,9 @@ __device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const flo
     const double cL = repl[hh], cR = repl[hh + 2];
     const double gs = (double)sg[cl] / (cR - cL);
     const double kl = scoef[cl * K + l], kr = scoef[cl * K + r];
-    const double A = gs * (kl * (cR + (double)sdd[cl * K + l]) - kr * (cL + (double)sdd[cl * K + r]));
+    const double dl = (double)sdd[cl * K + l] + (double)sdl[cl * K + l];
+    const double dr = (double)sdd[cl * K + r] + (double)sdl[cl * K + r];
+    const double A = gs * (kl * (cR + dl) - kr * (cL + dr));
     const double Bc = 2.0 * gs * (kr - kl);
     const float e = hh == 0 ? 0.0f : tab[hh];
     const float4 v = make_float4((float)(A + Bc * (double)e), (float)(A + Bc * ((double)e - 0.5)),
@@ -1984,16 +2037,7 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
     softmax_fast<C>(p);
     float gp[C];
     uint32_t lab = 0xffffffffu;
-    // soft: half the rounding error of the labelled channel's float32
-    // residual p - 1 (see below), once per voxel
-    float hrho = 0.0f;
-    if constexpr (SOFT) {
-      lab = fast_label<C>(t.lab[j]);
-      float pl = p[0];
-#pragma unroll
-      for (int c = 1; c < C; ++c) pl = lab == (uint32_t)c ? p[c] : pl;
-      hrho = 0.5f * (((pl - 1.0f) + 1.0f) - pl);
-    }
+    if constexpr (SOFT) lab = fast_label<C>(t.lab[j]);
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       gp[c] = 0.0f;
@@ -2006,14 +2050,7 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
         const int h = bucket_unit<RIGHT>(p[c], nf, tab);
         const float4 ab = *reinterpret_cast<const float4*>(sab + 4 * (cl * 2 * K + h));
         const bool hit = lab == (uint32_t)c;
-        // the reference's residual is the float32 p - y (v2_autograd.py:
-        // 94-104); for y = 1 it is p - 1 + rho with rho = (fl(p - 1) + 1) - p,
-        // exact (fl(p - 1) + 1 and p are within a factor two, or the former
-        // is 0), and the linear form, exact in p - y, adds B/2 rho: t = p - e
-        // (exact) plus rho/2, rounded once (an error below 2^-24 t).  In a bin
-        // of one voxel d = fl(p - y) then cancels the residual exactly.
-        const float tt = (p[c] - ab.w) + (hit ? hrho : 0.0f);
-        gp[c] = fmaf(ab.z, tt, hit ? ab.y : ab.x);
+        gp[c] = fmaf(ab.z, p[c] - ab.w, hit ? ab.y : ab.x);
       }
     }
     float dot = 0.0f;
@@ -2039,11 +2076,12 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
 
   const size_t tab_floats = (size_t)(((n + 2) + (SOFT ? 2 * K + 2 : 0) + 3) / 4 * 4);
   float* scoef = tabs + tab_floats;
-  float* sdd = scoef + CK;
-  float* sg = sdd + (SOFT ? CK : 0);
+  float* sdd = scoef + CK;  // soft: d rounded to float32 (diff[0])
+  float* sdl = sdd + CK;    // soft: its remainder (diff[1])
+  float* sg = sdd + (SOFT ? 2 * CK : 0);
   // soft: (A_0, A_1, B, e) per half-bin, 16-byte aligned after g (tab_floats
   // is a multiple of 4; the host sizes the region the same way)
-  float* sab = tabs + (((size_t)tab_floats + (size_t)CK * (SOFT ? 2 : 1) + CL + 3) & ~(size_t)3);
+  float* sab = tabs + (((size_t)tab_floats + (size_t)CK * (SOFT ? 3 : 1) + CL + 3) & ~(size_t)3);
   const int nrepl = SOFT ? 2 * K + 2 : 0;
 
   const int64_t N = P.N;
@@ -2067,11 +2105,13 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
   treg.load(P.btab, P.rtab, n, nrepl, kThreads);
   const float* cb = P.coef + (int64_t)b * CK;
   const float* db = P.d + (int64_t)b * CK;
+  const float* dlb = db + (int64_t)P.B * CK;
   // unconditional loads (clamped indices) so that the waits below stay partial
   const int tc_ = min(tid, CK - 1);
   const int tl_ = min(tid, CL - 1);
   const float c0 = cb[tc_];
   const float d0 = SOFT ? db[tc_] : 0.0f;
+  const float dl0 = SOFT ? dlb[tc_] : 0.0f;
   const float g0 = P.jac[b * CL + tl_] * P.go[P.go_per_class ? b * CL + tl_ : 0];
   FastTile<C, VEC> ta, tb;
   const uint32_t v0 = (uint32_t)(tid * VEC);
@@ -2090,12 +2130,18 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
   treg.store(tabs, P.btab, P.rtab, n, nrepl, kThreads);
   if (tid < CK) {
     scoef[tid] = c0;
-    if (SOFT) sdd[tid] = d0;
+    if (SOFT) {
+      sdd[tid] = d0;
+      sdl[tid] = dl0;
+    }
   }
   if (tid < CL) sg[tid] = g0;
   for (int i = tid + kThreads; i < CK; i += kThreads) {
     scoef[i] = cb[i];
-    if (SOFT) sdd[i] = db[i];
+    if (SOFT) {
+      sdd[i] = db[i];
+      sdl[i] = dlb[i];
+    }
   }
   for (int i = tid + kThreads; i < CL; i += kThreads)
     sg[i] = P.jac[b * CL + i] * (P.go_per_class ? P.go[b * CL + i] : P.go[0]);
@@ -2103,7 +2149,7 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
   const float* tab = tabs;
   const float* repl = tabs + n + 2;
   if constexpr (SOFT) {
-    soft_half_bin_coefficients(sab, tab, repl, scoef, sdd, sg, K, CL);
+    soft_half_bin_coefficients(sab, tab, repl, scoef, sdd, sdl, sg, K, CL);
     __syncthreads();
   }
 

@@ -88,6 +88,10 @@ size_t ace_workspace_reset_bytes(int64_t batch, int64_t channels,
  * Forward: per-bin statistics (W, P, G) of every (b, c') slice, then the
  * epilogue (reference kernels/epilogue.py:23-82 semantics):
  *   d[b,c',k]    = P/W - G/W for non-empty bins, else 0            [B, C', K]
+ *                  soft binning: `diff` holds [2, B, C', K], d rounded to
+ *                  float32 (diff[0]) and d minus that rounding (diff[1]),
+ *                  so that the backward's p - y - d keeps the precision of
+ *                  the float64 sums; hard: [B, C', K], d in float32
  *   coef[b,c',k] = sign(d) / (K_ne * W) for non-empty bins, else 0 [B, C', K]
  *   per_class    = f * present * w_c   (f = mean |d| over non-empty bins,
  *                  NaN when every bin is empty)                    [B, C']
@@ -114,7 +118,9 @@ int ace_forward(const void* x, int x_dtype, const void* target,
  * Backward: dx[b,c,n] = d loss / d x for upstream gradient `grad_output`
  * (one float32 scalar when grad_output_per_class == 0, else [B, C'] values,
  * reduction NONE).  g = jac * grad_output is formed in-kernel.  `coef`, `diff`
- * and `jac` are the forward's outputs; `diff` may be NULL for hard binning.
+ * and `jac` are the forward's outputs (soft: both parts of `diff`, 2 B C' K
+ * values; a caller holding only a float32 d passes zeros as its remainder);
+ * `diff` may be NULL for hard binning.
  * `target` may be NULL for hard binning (the hard gradient does not use it).
  * dx has the element type of x.
  */
@@ -291,6 +297,21 @@ int ace_set_timeline(void* stamps);
  * ACE_EINVAL for max_polls > 2^20 or publish_delay > 2^16, else ACE_OK.
  */
 int ace_set_test_hooks(int max_polls, int publish_delay);
+
+/*
+ * Test hook; no counterpart in the reference.  ace_probabilities writes the
+ * probabilities that every forward and backward kernel computes from x --
+ * softmax over channels (max, exp, the sum in channel order, the IEEE
+ * quotient), sigmoid, or x itself (ACE_ACT_*) -- as float32 [B, C, N] into
+ * `p`, one asynchronous launch on `stream`.  The parity tests measure with it
+ * how far the float32 rounding of the probabilities (the kernels' against
+ * torch's) moves a loss or gradient.  Returns ACE_EINVAL for null pointers,
+ * a bad dtype or activation, ACE_EUNSUPPORTED for C > 64, else ACE_OK or a
+ * HIP error.
+ */
+int ace_probabilities(const void* x, int x_dtype, int64_t batch,
+                      int64_t channels, int64_t voxels, int activation,
+                      float* p, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,29 @@ def run(impl: str, x: torch.Tensor, y: torch.Tensor, config: ACEConfig, upstream
     return loss.detach(), grad
 
 
+_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}  # ACE_F32, ACE_BF16, ACE_F16
+
+
+def kernel_probs(x: torch.Tensor, config: ACEConfig) -> torch.Tensor:
+    """The kernels' own float32 probabilities of logits x, on the CPU:
+    ``ace_probabilities`` runs the activation that every forward and backward
+    kernel applies (softmax: max, exp, the sum in channel order, the IEEE
+    quotient; it differs from torch's CPU softmax by an ulp on a few per cent
+    of the probabilities)."""
+    from ace_kernels import _lib
+
+    xc = x.detach().cuda().contiguous()
+    c = xc.shape[1]
+    act = {"softmax": _lib.ACT_SOFTMAX if c > 1 else _lib.ACT_NONE,
+           "sigmoid": _lib.ACT_SIGMOID}.get(config.activation, _lib.ACT_NONE)
+    p = torch.empty(xc.shape, dtype=torch.float32, device=xc.device)
+    n = xc[0, 0].numel()
+    rc = _lib.lib().ace_probabilities(xc.data_ptr(), _DTYPES[xc.dtype], xc.shape[0], c, n, act,
+                                      p.data_ptr(), hip._stream(xc.device))
+    _lib.check(rc, "ace_probabilities")
+    return p.cpu()
+
+
 def truth64(x: torch.Tensor, y: torch.Tensor, config: ACEConfig, upstream=None):
     """(loss, grad) in float64 throughout: the oracle's v2 path (the
     handwritten gradient of ``impls/v2_autograd.py``) on float64 logits on

@@ -227,3 +227,19 @@ def test_autograd_source_reaches_kernels_through_the_c_abi() -> None:
     assert '#include "ace_hip.h"' in src
     for name in ("hipLaunchKernel", "<<<", "hipMalloc", "hipMemset"):
         assert name not in src, name
+
+
+def test_probabilities_hook_checks_its_arguments() -> None:
+    """ace_probabilities validates before any HIP call: bad sizes, dtype or
+    activation and null pointers are ACE_EINVAL, C > 64 ACE_EUNSUPPORTED, and
+    an empty problem launches nothing (ACE_OK with null pointers)."""
+    lib = _lib.lib()
+    fake = 256
+    assert lib.ace_probabilities(fake, _lib.F32, 1, 0, 8, _lib.ACT_SOFTMAX, fake, None) == _lib.EINVAL
+    assert lib.ace_probabilities(fake, _lib.F32, -1, 4, 8, _lib.ACT_SOFTMAX, fake, None) == _lib.EINVAL
+    assert lib.ace_probabilities(fake, _lib.F32, 1, 4, 8, 3, fake, None) == _lib.EINVAL
+    assert lib.ace_probabilities(fake, _lib.F32, 1, 65, 8, _lib.ACT_SOFTMAX, fake, None) == _lib.EUNSUPPORTED
+    assert lib.ace_probabilities(None, _lib.F32, 1, 4, 8, _lib.ACT_SOFTMAX, fake, None) == _lib.EINVAL
+    assert lib.ace_probabilities(fake, _lib.F32, 1, 4, 8, _lib.ACT_SOFTMAX, None, None) == _lib.EINVAL
+    assert lib.ace_probabilities(fake, _lib.F64, 1, 4, 8, _lib.ACT_SOFTMAX, fake, None) == _lib.EINVAL
+    assert lib.ace_probabilities(None, _lib.F32, 0, 4, 8, _lib.ACT_SOFTMAX, None, None) == 0

@@ -7,21 +7,23 @@ small residual, and in a bin whose weight is just above ``empty_weight``
 the coefficient 1 / (K_ne W) is large as well.  The cases below are the
 ones randomized sweeps of the option space found beyond the bars before the
 fixes of the moments backward (evaluated from each half-bin's lower
-boundary, with the float32 residual's rounding), of the soft epilogue's d
-(float32 quotients of the float64 sums) and of the generic soft sums (up to
-40 fraction bits): the recorded K = 23, B = 4, C = 4, 15-voxel, logit scale
-10 case, other moments-path cases (C in {3, 4, 16}, right edges, class
-weights) and generic-kernel cases (one-hot targets, 5, 8 and 17 channels).
-Then a seeded sweep at logit scale 10 (saturated softmax) over fast and
-generic kernels, label and one-hot targets.
+boundary), of d (carried as float64 through to the backward, as its float32
+rounding and the remainder), of the generic soft forward (exact-arithmetic
+weights summed at up to 40 fraction bits) and of this rule's probability
+spread: the recorded K = 23, B = 4, C = 4, 15-voxel, logit scale 10 case,
+other moments-path cases (C in {3, 4, 16}, right edges, class weights) and
+generic-kernel cases (one-hot targets, 5, 8 and 17 channels).  Then a
+seeded sweep at logit scale 10 (saturated softmax) over fast and generic
+kernels, label and one-hot targets.
 
 Two float32 softmaxes of the same logits differ in the last place: torch's
-CPU softmax (the oracle's) and the kernels' IEEE quotient (as the
-reference's own GPU kernels divide, ``kernels/act.py:56-62``) disagree by
-one or two units on a few per cent of the probabilities, and in these bins
-the gradient moves by up to a few 1e-6 with them.  ``_rounding_spread``
-measures that: the float64 gradient (the oracle's v2 path) at torch's
-probabilities against the float64 gradient at the kernels' rounding.
+CPU softmax (the oracle's) and the kernels' (exp_neg, within an ulp, and the
+IEEE quotient, as the reference's own GPU kernels divide,
+``kernels/act.py:56-62``) disagree by one or two units on a few per cent of
+the probabilities, and in these bins the gradient moves by up to a few 1e-6
+with them.  ``_rounding_spread`` measures that: the float64 gradient (the
+oracle's v2 path) at torch's probabilities against the float64 gradient at
+the kernels' own (``ace_probabilities``).
 
 Each element must pass (voxels within 1e-6 of a bin boundary may differ,
 and must be rare, as in ``gpu_helpers.assert_grad_close``):
@@ -44,7 +46,8 @@ import torch
 
 from ace_kernels import ACEConfig
 from ace_kernels import measure as m
-from gpu_helpers import GRAD_ATOL, GRAD_RTOL, LOSS_ATOL, LOSS_RTOL, near_boundary_voxels, run, say, truth64
+from gpu_helpers import (GRAD_ATOL, GRAD_RTOL, LOSS_ATOL, LOSS_RTOL, kernel_probs, near_boundary_voxels, run,
+                         say, truth64)
 
 pytestmark = pytest.mark.gpu
 
@@ -76,6 +79,25 @@ RECORDED = [
                                           "ignore_empty_classes": False, "reduction": "none"}),
     (1, 4, (14, 21), 10.0, 0.0, 1513345875, {"num_bins": 49, "to_onehot_y": False, "ignore_empty_classes": False,
                                              "reduction": "none", "right": True}),
+    # beyond the rule while d reached the backward as float32 (and the
+    # residual carried the rounding of p - 1), the generic forward summed
+    # float32 weights, and the rounding spread assumed a correctly rounded exp
+    (2, 16, (21, 10), 0.5, 2.0, 1748988274, {"num_bins": 44, "include_background": False, "reduction": "sum",
+                                             "right": True}),
+    (1, 16, (6, 3, 12), 10.0, 0.0, 2070347628, {"num_bins": 52, "ignore_empty_classes": False, "reduction": "sum",
+                                                "weight": 0.5}),
+    (3, 4, (20, 14, 5), 0.5, 0.0, 2141653390, {"num_bins": 43, "include_background": False, "reduction": "sum",
+                                               "weight": 0.5, "right": True}),
+    (3, 16, (13, 8, 10), 10.0, 2.0, 7752191, {"num_bins": 35, "reduction": "sum", "weight": 0.5, "right": True}),
+    (2, 16, (9, 13), 2.0, 0.0, 1216471979, {"num_bins": 43, "ignore_empty_classes": False, "reduction": "sum",
+                                            "weight": 0.5, "right": True}),
+    (4, 4, (23, 8, 3), 0.5, 0.0, 1389469926, {"num_bins": 56, "include_background": False,
+                                              "ignore_empty_classes": False, "reduction": "sum", "weight": 0.5,
+                                              "right": True}),
+    (1, 17, (19, 14, 3), 2.0, 0.0, 739499247, {"num_bins": 53, "reduction": "none", "weight": 0.5}),
+    (4, 17, (5, 19, 7), 10.0, 2.0, 1818557503, {"num_bins": 47, "reduction": "none", "right": True}),
+    (3, 17, (20, 18, 3), 2.0, 2.0, 1241132347, {"num_bins": 58, "include_background": False,
+                                                "ignore_empty_classes": False, "reduction": "none"}),
 ]
 
 
@@ -93,16 +115,11 @@ def _grad64_at(p: torch.Tensor, y: torch.Tensor, cfg: ACEConfig) -> torch.Tensor
 
 def _rounding_spread(x: torch.Tensor, y: torch.Tensor, cfg: ACEConfig) -> torch.Tensor:
     """|float64 gradient at torch's float32 softmax - float64 gradient at the
-    kernels' rounding (exp rounded to float32, the sum in channel order, the
-    IEEE quotient)| per element."""
+    kernels' own float32 probabilities (``ace_probabilities``)| per element."""
     if cfg.activation != "softmax" or x.shape[1] == 1:
         return torch.zeros(x.shape, dtype=torch.float64)
     xf = x.float()
-    e = torch.exp((xf - xf.max(1, keepdim=True).values).double()).float()
-    s = e[:, :1].clone()
-    for c in range(1, e.shape[1]):
-        s = s + e[:, c:c + 1]
-    return (_grad64_at(torch.softmax(xf, 1), y, cfg) - _grad64_at(e / s, y, cfg)).abs()
+    return (_grad64_at(torch.softmax(xf, 1), y, cfg) - _grad64_at(kernel_probs(xf, cfg), y, cfg)).abs()
 
 
 def _check(shape: m.ShapeSpec, seed: int, cfg: ACEConfig) -> None:

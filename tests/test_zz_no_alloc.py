@@ -40,7 +40,7 @@ def _noalloc(pl, config: ACEConfig):
     dev = pl.x.device
     f32 = torch.float32
     coef = torch.empty((pl.B, pl.CL, pl.K), dtype=f32, device=dev)
-    d = torch.empty_like(coef)
+    d = torch.empty(hip._d_shape(pl), dtype=f32, device=dev)  # soft: d and its remainder
     jac = torch.empty((pl.B, pl.CL), dtype=f32, device=dev)
     per_class = torch.empty((pl.B, pl.CL), dtype=f32, device=dev)
     reduction = hip._REDUCTIONS[config.reduction]
@@ -130,7 +130,7 @@ def test_noalloc_replays_under_graph_capture(binning: str) -> None:
     pl = hip.make_plan(x, y, config)
     want = hip.hip_forward(pl, config, stats=True, shared=False)
     dev = x.device
-    outs = (torch.empty((pl.B, pl.CL, pl.K), device=dev), torch.empty((pl.B, pl.CL, pl.K), device=dev),
+    outs = (torch.empty((pl.B, pl.CL, pl.K), device=dev), torch.empty(hip._d_shape(pl), device=dev),
             torch.empty((pl.B, pl.CL), device=dev), torch.empty((pl.B, pl.CL), device=dev),
             torch.empty((), device=dev), torch.empty((3, pl.B, pl.CL, pl.K), dtype=torch.float64, device=dev))
     say(f"noalloc graph {binning}: warm call")
