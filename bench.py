@@ -648,6 +648,26 @@ def _profile_key(name: str, workloads):
     return None
 
 
+def _summarize_trace(durations) -> None:
+    """Markdown table of a rocprofv3 ``--kernel-trace`` run: per ace kernel and
+    workload the dispatch count and durations (ns), its algorithmic bytes
+    (forward: logits + labels; backward: logits read and gradient written,
+    plus labels for soft binning) and the rate at the average duration."""
+    from ace_kernels.workloads import workload
+
+    print("| kernel | workload | calls | average ns | median ns | min ns | max ns | algorithmic bytes | "
+          "GB/s at average |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|")
+    for (kernel, idx), v in sorted(durations.items(), key=lambda kv: (kv[0][1], kv[0][0])):
+        wl = workload(idx)
+        xb, tb = wl.input_bytes(), wl.target_bytes()
+        algo = xb + tb if kernel == "ace_fwd" else 2 * xb + (tb if wl.config.binning == "soft" else 0)
+        avg = statistics.fmean(v)
+        print(f"| {kernel} | cfg{idx} {wl.config.binning} | {len(v)} | {avg:.0f} | {statistics.median(v):.0f} | "
+              f"{min(v)} | {max(v)} | {algo} | {algo / avg:.0f} |")
+    print()
+
+
 def summarize_profiles(dirs, workloads) -> int:
     """Summarise rocprofv3 ``--pmc`` runs of ``bench.py --profile-kernels``
     (the ``*counter_collection.csv`` files under ``dirs``): the median of each
@@ -658,7 +678,7 @@ def summarize_profiles(dirs, workloads) -> int:
     with the hash of the kernel sources they were measured on."""
     import csv
 
-    values = {}
+    values, durations = {}, {}
     for d in dirs:
         for f in sorted(Path(d).rglob("*counter_collection.csv")):
             with open(f, newline="") as fh:
@@ -667,8 +687,19 @@ def summarize_profiles(dirs, workloads) -> int:
                     if key is not None:
                         values.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(
                             float(r["Counter_Value"]))
+        for f in sorted(Path(d).rglob("*kernel_trace.csv")):
+            with open(f, newline="") as fh:
+                for r in csv.DictReader(fh):
+                    key = _profile_key(r["Kernel_Name"], workloads)
+                    if key is not None and key[0] != "copy":
+                        durations.setdefault(key, []).append(
+                            int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    if durations:
+        _summarize_trace(durations)
     if not values:
-        print("no counter_collection.csv rows of the ace kernels found", file=sys.stderr)
+        if durations:
+            return 0
+        print("no counter_collection.csv or kernel_trace.csv rows of the ace kernels found", file=sys.stderr)
         return 1
 
     def copy_median(counter: str):
@@ -796,7 +827,8 @@ def main() -> int:
     ap.add_argument("--timeline", type=int, default=0, metavar="LAUNCHES",
                     help="print the per-block phase timeline of LAUNCHES cold forwards (markdown)")
     ap.add_argument("--summarize-profiles", nargs="+", metavar="DIR",
-                    help="summarise rocprofv3 --pmc runs of --profile-kernels (no GPU needed)")
+                    help="summarise rocprofv3 --pmc runs of --profile-kernels and --kernel-trace runs "
+                         "of bench.py (no GPU needed)")
     args = ap.parse_args()
     if args.summarize_profiles:
         sys.path.insert(0, str(ROOT / "ace-kernels_amd"))
