@@ -193,3 +193,24 @@ def test_target_that_needs_a_gradient_gets_none() -> None:
         loss = ace_loss(leaf, t, cfg, impl="hip_mi355x")
         loss.backward()
         assert t.grad is None and torch.equal(leaf.grad, want)
+
+
+def test_soft_d_without_its_remainder() -> None:
+    """The soft forward's d is [2, B, C', K]: its float32 rounding and the
+    remainder, which the backward adds.  A plain [B, C', K] float32 d (no
+    remainder) gives the same gradient as the two-part d with a zero
+    remainder, within float32 rounding of the full one; a d of any other
+    size is refused before a launch."""
+    cfg = ACEConfig(binning="soft", num_bins=20, to_onehot_y=True)
+    x, y = _inputs(seed=23)
+    pl = hip.make_plan(x, y, cfg)
+    loss, coef, d, jac, _, _ = hip.hip_forward(pl, cfg)
+    assert d.shape == (2, pl.B, pl.CL, pl.K)
+    go = torch.ones_like(loss)
+    full = hip.hip_backward(pl, coef, d, jac, go)
+    plain = hip.hip_backward(pl, coef, d[0].clone(), jac, go)
+    zero_lo = torch.stack([d[0], torch.zeros_like(d[0])]).contiguous()
+    assert torch.equal(plain, hip.hip_backward(pl, coef, zero_lo, jac, go))
+    torch.testing.assert_close(plain, full, rtol=1e-4, atol=1e-7)
+    with pytest.raises(ValueError, match="d must be"):
+        hip.hip_backward(pl, coef, d[:, :1].contiguous(), jac, go)
