@@ -4,9 +4,11 @@ Mirrors the reference's fastest implementation, ``_V6Loss``
 (``src/ace_kernels/impls/v6_triton.py:93-111``, with ``_forward`` ``:43-65``
 and ``_backward`` ``:68-90``): logits in (float32 / bfloat16 / float16),
 d logits out in the logits' dtype; saved for backward are the inputs
-(already held by the caller) plus ``coef``, ``d`` ``[B, C', K]`` and ``jac``
-``[B, C']``.  The forward is one kernel launch (histograms, cross-block
-reduction and epilogue); the backward is one launch.
+(already held by the caller) plus ``coef`` ``[B, C', K]``, ``d`` (``[B, C',
+K]``; soft binning ``[2, B, C', K]``, d rounded to float32 and its
+remainder) and ``jac`` ``[B, C']``.  The forward is one kernel launch
+(histograms, cross-block reduction and epilogue); the backward is one
+launch.
 
 Input handling follows ``as_kernel_input`` (``kernels/act.py:69-73``) and
 ``_kernel_target`` (``impls/v5_triton.py:25-32``): logits are viewed as

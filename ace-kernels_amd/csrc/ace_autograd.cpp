@@ -53,7 +53,8 @@ struct Signature {
   const float* centre_table = nullptr;
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
-  // `saved` (float32): coef [B, C', K] at 0, d at o_d, jac [B, C'] at o_jac,
+  // `saved` (float32): coef [B, C', K] at 0, d at o_d ([B, C', K], soft
+  // [2, B, C', K]: its float32 rounding and remainder), jac [B, C'] at o_jac,
   // and the per-class errors at o_pc unless they are the returned loss
   int64_t n_saved = 0, o_d = 0, o_jac = 0, o_pc = 0;
   bool reduced = true, soft = false;
