@@ -39,7 +39,10 @@ and must be rare, as in ``gpu_helpers.assert_grad_close``):
 - the reference's GPU bar, rtol 1e-3 / atol 1e-6 (``tests/helpers.py:
   17-21``), widened by the rounding spread (the float64 gradient at torch's
   probabilities against the one at the kernels'), or be at least as close to
-  the float64 result as the float32 reference is;
+  the float64 result as the float32 reference is, or be within the tolerance
+  below of the float64 oracle at the kernels' own probabilities (where the
+  float32 reference's own arithmetic is beyond its GPU bar of the exact
+  result at its probabilities);
 - the north star's rtol 1e-4 (1e-3 below 8 voxels per bin, the reference's
   own few-voxel rule, ``tests/test_triton.py:289-290``) / atol 1e-7 against
   the float32 reference, or against the float64 oracle at the kernels' own
@@ -111,6 +114,9 @@ RECORDED = [
     (4, 17, (5, 19, 7), 10.0, 2.0, 1818557503, {"num_bins": 47, "reduction": "none", "right": True}),
     (3, 17, (20, 18, 3), 2.0, 2.0, 1241132347, {"num_bins": 58, "include_background": False,
                                                 "ignore_empty_classes": False, "reduction": "none"}),
+    # the float32 reference 1.2e-6 from the exact result at its own
+    # probabilities, beyond its GPU bar; HIP 2e-10 from it at the kernels'
+    (4, 3, (15,), 0.5, 2.0, 1270373627, {"num_bins": 53, "reduction": "sum", "right": True}),
 ]
 
 
@@ -156,10 +162,11 @@ def _check(shape: m.ShapeSpec, seed: int, cfg: ACEConfig) -> None:
         loss_exact = (lc - lk).abs() <= LOSS_RTOL * lk.abs() + LOSS_ATOL
         assert (loss_closer | loss_exact).all(), (lc, lr, loss64, lk)
     spread = (at_torch - own).abs()  # torch's float32 softmax against the kernels'
-    bar = ((g - r).abs() <= 1e-3 * r.abs() + 1e-6 + spread) | closer
+    # within tolerance of the exact result for the kernels' own inputs
+    exact = (g - own).abs() <= rtol * own.abs() + GRAD_ATOL
+    bar = ((g - r).abs() <= 1e-3 * r.abs() + 1e-6 + spread) | closer | exact
     tol = rtol * t.abs() + GRAD_ATOL
     conditioned = ((r - t).abs() > tol) | (spread > tol)
-    exact = (g - own).abs() <= rtol * own.abs() + GRAD_ATOL
     strict = torch.isclose(g, r, rtol=rtol, atol=GRAD_ATOL) | closer | conditioned | exact
     bad = (~(bar & strict)).flatten(2).any(1)
     if bad.any():
