@@ -532,6 +532,14 @@ struct TableRegs {
 // per-channel targets.  `load` issues the vector loads only; the values are
 // first used by the binning, so a load can be in flight while another tile is
 // processed.
+// Whether a generic kernel streams two tiles in rotation (software
+// pipelining).  The soft kernels at one voxel per lane with 16 or more
+// channels do not: their per-voxel arrays leave no room for a second tile.
+template <int CMAX, int VEC, bool SOFT>
+constexpr bool generic_pipelined() {
+  return !(SOFT && VEC == 1 && CMAX >= 16);
+}
+
 template <int CMAX, int VEC>
 struct Tile {
   float x[CMAX][VEC];
@@ -1305,11 +1313,16 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
   const T* xt = reinterpret_cast<const T*>(P.x) + (int64_t)b * nc * N + t0;
   const long long* lt = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
   const float* yt = reinterpret_cast<const float*>(P.tgt) + (int64_t)b * nc * N + t0;
-  const int nfull = P.vec_ok ? nvox / VEC * VEC : 0;
+  // generic soft kernels with one voxel per lane and 16 or more channels
+  // bin every voxel in the single-voxel loop below: two tiles in flight held
+  // their logits and targets twice (204 VGPRs at 32 channels, 2 waves per
+  // SIMD); occupancy hides the loads instead
+  constexpr bool kPipe = generic_pipelined<CMAX, VEC, SOFT>();
+  const int nfull = (kPipe && P.vec_ok) ? nvox / VEC * VEC : 0;
 
   // full vector steps, software-pipelined: the next step's loads are in flight
   // while the current step is binned (two buffers, unrolled by two)
-  {
+  if constexpr (kPipe) {
     Tile<CMAX, VEC> ta, tb;
     const int stride = kThreads * VEC;
     int v = tid * VEC;
@@ -1322,6 +1335,9 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
         fwd_accumulate<CMAX, EXACT, VEC, SOFT, RIGHT>(P, H, btab, repl, nc, copy, tb.x, tb.lab, tb.y, labels);
     }
   }
+  // one voxel per iteration, not unrolled (the registers of one voxel's
+  // channels; the generic soft kernels take every voxel here)
+#pragma unroll 1
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     float xv[CMAX][1];
 #pragma unroll
@@ -1420,7 +1436,8 @@ __device__ __forceinline__ void bwd_load(Tile<CMAX, VEC>& t, const T* xt, const 
 }
 
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
-__global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
+__global__ void __launch_bounds__(kThreads)
+    bwd_kernel(const BwdParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* tabs = reinterpret_cast<float*>(smem);
   const int K = P.K;
@@ -1464,10 +1481,14 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
   T* dt = reinterpret_cast<T*>(P.dx) + (int64_t)b * nc * N + t0;
   const long long* lt = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
   const float* yt = reinterpret_cast<const float*>(P.tgt) + (int64_t)b * nc * N + t0;
-  const int nfull = P.vec_ok ? nvox / VEC * VEC : 0;
+  // as in the forward: the generic soft kernels at one voxel per lane with 16
+  // or more channels take every voxel through the single-voxel loop (two
+  // tiles plus the probabilities and dL/dp held 340 VGPRs at 32 channels)
+  constexpr bool kPipe = generic_pipelined<CMAX, VEC, SOFT>();
+  const int nfull = (kPipe && P.vec_ok) ? nvox / VEC * VEC : 0;
 
   // full vector steps, software-pipelined as in the forward
-  {
+  if constexpr (kPipe) {
     Tile<CMAX, VEC> ta, tb;
     const int stride = kThreads * VEC;
     // the hard gradient needs no targets: only the logits are loaded
@@ -1491,6 +1512,9 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(const BwdParams P) {
       }
     }
   }
+  // one voxel per iteration, not unrolled (the registers of one voxel's
+  // channels; the generic soft kernels take every voxel here)
+#pragma unroll 1
   for (int v = nfull + tid; v < nvox; v += kThreads) {
     float xv[CMAX][1];
 #pragma unroll
@@ -2402,8 +2426,12 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
     }                                                                                \
   } else {                                                                           \
     switch (v.cmax) {                                                                \
-      case 8: return LAUNCH<T, 8, false, 4, SOFT, RIGHT>(g, p, s);                   \
-      case 16: return LAUNCH<T, 16, false, 4, SOFT, RIGHT>(g, p, s);                 \
+      case 8:                                                                        \
+        if constexpr (SOFT) return LAUNCH<T, 8, false, 1, SOFT, RIGHT>(g, p, s);     \
+        else return LAUNCH<T, 8, false, 4, SOFT, RIGHT>(g, p, s);                    \
+      case 16:                                                                       \
+        if constexpr (SOFT) return LAUNCH<T, 16, false, 1, SOFT, RIGHT>(g, p, s);    \
+        else return LAUNCH<T, 16, false, 4, SOFT, RIGHT>(g, p, s);                   \
       case 32: return LAUNCH<T, 32, false, 1, SOFT, RIGHT>(g, p, s);                 \
       case 64: return LAUNCH<T, 64, false, 1, SOFT, RIGHT>(g, p, s);                 \
     }                                                                                \
@@ -2422,6 +2450,11 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
   template <>                                                                        \
   hipError_t launch_variant_bwd<T, SOFT, RIGHT>(const Geometry& g, const BwdParams& p, \
                                                 hipStream_t s) {                     \
+    /* the generic soft backward for 9-16 channels runs the 32-channel kernel   \
+       (176 VGPRs, two waves per SIMD; the 16-channel one took 272, one wave) */ \
+    if constexpr (SOFT)                                                              \
+      if (!g.var.exact && g.var.cmax == 16)                                          \
+        return launch_bwd_t<T, 32, false, 1, SOFT, RIGHT>(g, p, s);                  \
     ACE_VARIANT_SWITCH(launch_bwd_t, T, SOFT, RIGHT)                                 \
   }                                                                                  \
   template <>                                                                        \
