@@ -533,11 +533,11 @@ struct TableRegs {
 // first used by the binning, so a load can be in flight while another tile is
 // processed.
 // Whether a generic kernel streams two tiles in rotation (software
-// pipelining).  The soft kernels at one voxel per lane with 16 or more
-// channels do not: their per-voxel arrays leave no room for a second tile.
+// pipelining).  At one voxel per lane with 16 or more channels it does not:
+// the per-voxel arrays leave no room for a second tile.
 template <int CMAX, int VEC, bool SOFT>
 constexpr bool generic_pipelined() {
-  return !(SOFT && VEC == 1 && CMAX >= 16);
+  return !(VEC == 1 && CMAX >= 16);
 }
 
 template <int CMAX, int VEC>
@@ -1313,10 +1313,10 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(const FwdParams P) {
   const T* xt = reinterpret_cast<const T*>(P.x) + (int64_t)b * nc * N + t0;
   const long long* lt = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
   const float* yt = reinterpret_cast<const float*>(P.tgt) + (int64_t)b * nc * N + t0;
-  // generic soft kernels with one voxel per lane and 16 or more channels
-  // bin every voxel in the single-voxel loop below: two tiles in flight held
-  // their logits and targets twice (204 VGPRs at 32 channels, 2 waves per
-  // SIMD); occupancy hides the loads instead
+  // generic kernels with one voxel per lane and 16 or more channels bin
+  // every voxel in the single-voxel loop below: two tiles in flight held
+  // their logits and targets twice (soft: 204 VGPRs at 32 channels, 2 waves
+  // per SIMD); occupancy hides the loads instead
   constexpr bool kPipe = generic_pipelined<CMAX, VEC, SOFT>();
   const int nfull = (kPipe && P.vec_ok) ? nvox / VEC * VEC : 0;
 
@@ -1481,8 +1481,8 @@ __global__ void __launch_bounds__(kThreads)
   T* dt = reinterpret_cast<T*>(P.dx) + (int64_t)b * nc * N + t0;
   const long long* lt = reinterpret_cast<const long long*>(P.tgt) + (int64_t)b * N + t0;
   const float* yt = reinterpret_cast<const float*>(P.tgt) + (int64_t)b * nc * N + t0;
-  // as in the forward: the generic soft kernels at one voxel per lane with 16
-  // or more channels take every voxel through the single-voxel loop (two
+  // as in the forward: the generic kernels at one voxel per lane with 16 or
+  // more channels take every voxel through the single-voxel loop (soft: two
   // tiles plus the probabilities and dL/dp held 340 VGPRs at 32 channels)
   constexpr bool kPipe = generic_pipelined<CMAX, VEC, SOFT>();
   const int nfull = (kPipe && P.vec_ok) ? nvox / VEC * VEC : 0;
@@ -2426,12 +2426,8 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
     }                                                                                \
   } else {                                                                           \
     switch (v.cmax) {                                                                \
-      case 8:                                                                        \
-        if constexpr (SOFT) return LAUNCH<T, 8, false, 1, SOFT, RIGHT>(g, p, s);     \
-        else return LAUNCH<T, 8, false, 4, SOFT, RIGHT>(g, p, s);                    \
-      case 16:                                                                       \
-        if constexpr (SOFT) return LAUNCH<T, 16, false, 1, SOFT, RIGHT>(g, p, s);    \
-        else return LAUNCH<T, 16, false, 4, SOFT, RIGHT>(g, p, s);                   \
+      case 8: return LAUNCH<T, 8, false, 1, SOFT, RIGHT>(g, p, s);                   \
+      case 16: return LAUNCH<T, 16, false, 1, SOFT, RIGHT>(g, p, s);                 \
       case 32: return LAUNCH<T, 32, false, 1, SOFT, RIGHT>(g, p, s);                 \
       case 64: return LAUNCH<T, 64, false, 1, SOFT, RIGHT>(g, p, s);                 \
     }                                                                                \
@@ -2450,11 +2446,10 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
   template <>                                                                        \
   hipError_t launch_variant_bwd<T, SOFT, RIGHT>(const Geometry& g, const BwdParams& p, \
                                                 hipStream_t s) {                     \
-    /* the generic soft backward for 9-16 channels runs the 32-channel kernel   \
-       (176 VGPRs, two waves per SIMD; the 16-channel one took 272, one wave) */ \
-    if constexpr (SOFT)                                                              \
-      if (!g.var.exact && g.var.cmax == 16)                                          \
-        return launch_bwd_t<T, 32, false, 1, SOFT, RIGHT>(g, p, s);                  \
+    /* the generic backward for 9-15 channels runs the 32-channel kernel       \
+       (soft 176 / hard 140 VGPRs against 272 / 253 for the 16-channel one) */  \
+    if (!g.var.exact && g.var.cmax == 16)                                            \
+      return launch_bwd_t<T, 32, false, 1, SOFT, RIGHT>(g, p, s);                    \
     ACE_VARIANT_SWITCH(launch_bwd_t, T, SOFT, RIGHT)                                 \
   }                                                                                  \
   template <>                                                                        \

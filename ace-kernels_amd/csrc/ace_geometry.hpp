@@ -170,10 +170,10 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   // VGPRs instead of 100): on MI355X cfg 2's forward 26.7 vs 27.8 us; the
   // soft and backward kernels measured slower that way and keep four
   if (fast && !soft && C == 4) g.var.vec = 2;
-  // the generic soft kernels (5-16 channels) take one voxel per lane: at
-  // four their per-voxel soft assignment held 283 VGPRs (8 channels) or
-  // spilled (16), one wave per SIMD (the launchers instantiate them so)
-  if (soft && !g.var.exact) g.var.vec = 1;
+  // the generic kernels for 5-16 channels take one voxel per lane: at four,
+  // soft held 283 VGPRs at 8 channels and spilled at 16, hard 209 and 392
+  // (one or two waves per SIMD); the launchers instantiate them so
+  if (!g.var.exact) g.var.vec = 1;
   g.C = (int)C;
   g.off = (!include_background && C > 1) ? 1 : 0;
   g.CL = (int)C - g.off;
