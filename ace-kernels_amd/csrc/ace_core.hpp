@@ -408,9 +408,15 @@ __device__ __forceinline__ long long fx(float v) {
   return (long long)(int)rintf(v * 1073741824.0f);
 }
 // A float64 term |v| < 2 at scale sfx = 2^f (soft_frac: up to 2^40), rounded
-// to nearest: an error of at most 2^-(f+1) per term.
+// to nearest even: an error of at most 2^-(f+1) per term.  x = v sfx is exact
+// (a power-of-two scale) and |x| < 2^41, so x + 1.5 2^52 lies in [2^52, 2^53),
+// where the float64 spacing is 1: the add rounds x to the nearest even integer
+// and the difference of the bit patterns is that integer (rint and a float64
+// to int64 conversion, ~8 instructions, in 3).
 __device__ __forceinline__ long long fx_soft(double v, float sfx) {
-  return (long long)__builtin_rint(v * (double)sfx);
+  constexpr double kMagic = 0x1.8p52;
+  const double t = v * (double)sfx + kMagic;
+  return __double_as_longlong(t) - __double_as_longlong(kMagic);
 }
 
 __device__ __forceinline__ void lds_add(unsigned long long* p, unsigned long long v) {
