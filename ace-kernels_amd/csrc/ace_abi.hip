@@ -541,7 +541,7 @@ int ace_backward(const void* x, int x_dtype, const void* target, int target_kind
   const Geometry g = make_geometry(
       batch, channels, voxels, num_bins, soft, include_background != 0, labels,
       bwd_steps(soft, labels, act, batch, channels, voxels, include_background, moments), 0,
-      moments);
+      moments, false, kFastThreads, true);
   if (g.lds_bwd > kMaxLds) return ACE_EUNSUPPORTED;
   if (g.nblk > 0x7fffffffLL) return ACE_EUNSUPPORTED;
   if (voxels == 0) return ACE_OK;

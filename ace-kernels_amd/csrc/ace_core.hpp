@@ -2456,6 +2456,10 @@ hipError_t launch_bwd_levels_t(long long nblk, size_t lds, const BwdLevels& L, h
        (soft 176 / hard 140 VGPRs against 272 / 253 for the 16-channel one) */  \
     if (!g.var.exact && g.var.cmax == 16)                                            \
       return launch_bwd_t<T, 32, false, 1, SOFT, RIGHT>(g, p, s);                    \
+    /* the hard 5-8-channel backward: two voxels per lane (make_geometry) */      \
+    if constexpr (!SOFT)                                                             \
+      if (!g.var.exact && g.var.cmax == 8 && g.var.vec == 2)                         \
+        return launch_bwd_t<T, 8, false, 2, SOFT, RIGHT>(g, p, s);                   \
     ACE_VARIANT_SWITCH(launch_bwd_t, T, SOFT, RIGHT)                                 \
   }                                                                                  \
   template <>                                                                        \

@@ -162,7 +162,7 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
                               bool soft, bool include_background, bool labels,
                               int steps_override = 0, int copies_override = 0,
                               bool moments = false, bool fast = false,
-                              int max_nt = kFastThreads) {
+                              int max_nt = kFastThreads, bool backward = false) {
   Geometry g{};
   g.moments = moments;
   g.var = variant_for(C);
@@ -172,8 +172,11 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   if (fast && !soft && C == 4) g.var.vec = 2;
   // the generic kernels for 5-16 channels take one voxel per lane: at four,
   // soft held 283 VGPRs at 8 channels and spilled at 16, hard 209 and 392
-  // (one or two waves per SIMD); the launchers instantiate them so
-  if (!g.var.exact) g.var.vec = 1;
+  // (one or two waves per SIMD); the launchers instantiate them so.  The
+  // hard backward for 5-8 channels takes two (MI355X, B = 2, C = 5, 128^3:
+  // 58.3 us against 75.7 at one and 73.6 at four; every other generic kernel
+  // measured fastest at one)
+  if (!g.var.exact) g.var.vec = (backward && !soft && g.var.cmax == 8) ? 2 : 1;
   g.C = (int)C;
   g.off = (!include_background && C > 1) ? 1 : 0;
   g.CL = (int)C - g.off;
