@@ -2024,10 +2024,15 @@ __device__ __forceinline__ void fwd_fast_body(const FwdParams& P, const int64_t 
 // A_y = A + B (e - y/2) formed in float64 for y = 0 and y = 1, from
 // d = d_hi + d_lo (sdd, sdl: the float64 d of the forward's sums).  p - e is
 // exact in float32 (e <= p <= 2e for h >= 1, Sterbenz; e = 0 for h = 0) and
-// at most 1/(2K), so no float32 term is larger than dL/dp by more than ~2
-// coef g, and each voxel's dL/dp takes two roundings (A_y's and the fma's).
-// sab[4h .. 4h + 3] = (A_0, A_1, B, e) for half-bin h of every loss
-// channel; tab is the padded half-boundary table (tab[h] = e for h >= 1).
+// at most 1/(2K).  A_y and B (p - e) can still be many times dL/dp, which
+// they cancel to (bins whose weight is just above empty_weight, where coef
+// is large), so A_0, A_1 and B are each held as a float32 pair, value and
+// remainder: dL/dp = fma(B, p - e, A_y) + fma(B', p - e, A_y') is within an
+// ulp or two of dL/dp itself.  Per half-bin h of every loss channel (index
+// t = cl 2K + h): sab[8t + 4y .. 8t + 4y + 3] = (A_y, A_y', B, e) for y = 0
+// and y = 1, read by one 16-byte load at the voxel's y, and sbl[t] = B'
+// (sbl = sab + 8 C' 2K); tab is the padded half-boundary table (tab[h] = e
+// for h >= 1).
 __device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const float* tab,
                                                            const float* repl, const float* scoef,
                                                            const float* sdd, const float* sdl,
@@ -2046,9 +2051,11 @@ __device__ __forceinline__ void soft_half_bin_coefficients(float* sab, const flo
     const double A = gs * (kl * (cR + dl) - kr * (cL + dr));
     const double Bc = 2.0 * gs * (kr - kl);
     const float e = hh == 0 ? 0.0f : tab[hh];
-    const float4 v = make_float4((float)(A + Bc * (double)e), (float)(A + Bc * ((double)e - 0.5)),
-                                 (float)Bc, e);
-    *reinterpret_cast<float4*>(sab + 4 * t) = v;
+    const double a0 = A + Bc * (double)e, a1 = A + Bc * ((double)e - 0.5);
+    const float a0h = (float)a0, a1h = (float)a1, bh = (float)Bc;
+    *reinterpret_cast<float4*>(sab + 8 * t) = make_float4(a0h, (float)(a0 - (double)a0h), bh, e);
+    *reinterpret_cast<float4*>(sab + 8 * t + 4) = make_float4(a1h, (float)(a1 - (double)a1h), bh, e);
+    sab[8 * CL * H + t] = (float)(Bc - (double)bh);
   }
 }
 
@@ -2078,9 +2085,12 @@ __device__ __forceinline__ void fast_backward(FastTile<C, VEC>& t, const float* 
         gp[c] = scoef[cl * K + k] * sg[cl];
       } else {
         const int h = bucket_unit<RIGHT>(p[c], nf, tab);
-        const float4 ab = *reinterpret_cast<const float4*>(sab + 4 * (cl * 2 * K + h));
+        const int hb = cl * 2 * K + h;
         const bool hit = lab == (uint32_t)c;
-        gp[c] = fmaf(ab.z, p[c] - ab.w, hit ? ab.y : ab.x);
+        const float4 ab = *reinterpret_cast<const float4*>(sab + 8 * hb + (hit ? 4 : 0));
+        const float bl = sab[8 * (C - off) * 2 * K + hb];
+        const float t = p[c] - ab.w;
+        gp[c] = fmaf(ab.z, t, ab.x) + fmaf(bl, t, ab.y);
       }
     }
     float dot = 0.0f;
@@ -2109,8 +2119,9 @@ __device__ __forceinline__ void bwd_fast_body(const BwdParams& P, const int64_t 
   float* sdd = scoef + CK;  // soft: d rounded to float32 (diff[0])
   float* sdl = sdd + CK;    // soft: its remainder (diff[1])
   float* sg = sdd + (SOFT ? 2 * CK : 0);
-  // soft: (A_0, A_1, B, e) per half-bin, 16-byte aligned after g (tab_floats
-  // is a multiple of 4; the host sizes the region the same way)
+  // soft: (A_0, A_1, B, e) and their remainders per half-bin, 16-byte
+  // aligned after g (tab_floats is a multiple of 4; the host sizes the region
+  // the same way)
   float* sab = tabs + (((size_t)tab_floats + (size_t)CK * (SOFT ? 3 : 1) + CL + 3) & ~(size_t)3);
   const int nrepl = SOFT ? 2 * K + 2 : 0;
 

@@ -272,9 +272,9 @@ inline Geometry make_geometry(int64_t B, int64_t C, int64_t N, int K,
   const size_t region = hist > epi ? hist : epi;
   g.lds_fwd = g.tab_floats * 4 + region;
   // backward: tables + coef (+ d's two parts) + g, then for soft moments
-  // four values per half-bin from a 16-byte boundary (bwd_fast_body)
+  // nine values per half-bin from a 16-byte boundary (bwd_fast_body)
   g.lds_bwd = (align_up(g.tab_floats + (size_t)g.ck * (soft ? 3 : 1) + (size_t)g.CL, 4) +
-               (moments ? 8 * (size_t)g.ck : 0)) * 4;
+               (moments ? 18 * (size_t)g.ck : 0)) * 4;
   // workspace: ticket counters (groups, batch indices, loss), one loss
   // partial word per batch index and the final sums; it must start zero and
   // every call leaves it zero
