@@ -765,8 +765,8 @@ __device__ __forceinline__ void zero_sums(unsigned long long* fb, int NV, int re
 // Epilogue of batch indices [b0, b0 + nb) in one block.  Final sums -> W, P,
 // G per bin, d = P/W - G/W (kernels/epilogue.py:23-82); per class row: K_ne,
 // f, coef, jac (one wave per row).  It leaves its final sums zero and returns
-// (in thread 0, unless the reduction is "none") the sum of its rows'
-// per-class errors in row order.
+// (in wave 0, unless the reduction is "none") the sum of its rows'
+// per-class errors, in wave_sum's fixed order.
 template <bool SOFT, bool MOM>
 __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* hist,
                                           const float* repl, int CK, int CL, int b0, int nb) {
@@ -990,11 +990,17 @@ __device__ __forceinline__ float epilogue(const FwdParams& P, unsigned char* his
       if (lane == 0) row_tail(row, fcls, present);
     }
   }
+  // the rows' errors summed by wave 0 (every lane active): lane-strided, then
+  // wave_sum's fixed order, so the loss is bit-identical run to run (one LDS
+  // read and a DPP reduction instead of one dependent read per row)
   float total = 0.0f;
   if (P.red != kRedNone) {
     __syncthreads();
-    if (tid == 0)
-      for (int r = 0; r < nb * CL; ++r) total += sf[r];
+    if (tid < 64) {
+      float v = 0.0f;
+      for (int r = tid; r < nb * CL; r += 64) v += sf[r];
+      total = wave_sum(v);
+    }
   }
   return total;
 }
