@@ -2354,6 +2354,10 @@ hipError_t launch(Kern kern, long long nblk, size_t lds, hipStream_t s, const Pa
 
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) {
+  // the geometry's voxels per lane (tiles, the alignment test behind
+  // vec_ok) must be the kernel's: a wider kernel would issue vector loads
+  // the host never checked
+  if (g.var.vec != VEC) return hipErrorInvalidConfiguration;
   auto kern = fwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
   int nt = kThreads;
   if constexpr (has_fast<CMAX, EXACT>()) {
@@ -2378,6 +2382,7 @@ hipError_t launch_fwd_t(const Geometry& g, const FwdParams& prm, hipStream_t s) 
 
 template <typename T, int CMAX, bool EXACT, int VEC, bool SOFT, bool RIGHT>
 hipError_t launch_bwd_t(const Geometry& g, const BwdParams& prm, hipStream_t s) {
+  if (g.var.vec != VEC) return hipErrorInvalidConfiguration;  // as in launch_fwd_t
   auto kern = bwd_kernel<T, CMAX, EXACT, VEC, SOFT, RIGHT>;
   if constexpr (has_fast<CMAX, EXACT>()) {
     // the hard gradient reads no targets: any target layout takes the fast path
