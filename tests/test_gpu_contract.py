@@ -4,9 +4,10 @@
   forward with its fused epilogue, the backward) plus torch's glue, within
   the reference's bound of 8 device kernels (``tests/test_triton.py:453-471``).
 - Saved bytes: the autograd node keeps, beyond its inputs, exactly coef and d
-  (float32 [B, C', K]) and jac (float32 [B, C']):
-  2 B C' K 4 + B C' 4 bytes (``tests/test_triton.py:331-346``, which allows
-  up to 1 KB more; ``tests/test_saved_tensors.py``).
+  (float32 [B, C', K]; soft binning also keeps d's float32 remainder) and jac
+  (float32 [B, C']): 2 B C' K 4 + B C' 4 bytes hard, 3 B C' K 4 + B C' 4
+  soft (``tests/test_triton.py:331-346``, which allows up to 1 KB more;
+  ``tests/test_saved_tensors.py``).
 - torch.compile: the reference's pattern, ``torch.compile(step,
   fullgraph=True)`` with the default backend, where ``step`` is a network
   plus ``ace_loss(..., impl=...)`` through the custom ops; loss and weight
