@@ -479,6 +479,9 @@ __device__ __forceinline__ unsigned long long cas_dev(unsigned long long* p, uns
                                        __HIP_MEMORY_SCOPE_AGENT);
   return expected;  // the word's value before the exchange
 }
+__device__ __forceinline__ unsigned long long xchg_dev(unsigned long long* p, unsigned long long v) {
+  return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ int ticket(int* ctr) {
   return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1225,9 +1228,31 @@ __device__ __forceinline__ void fwd_finish(const FwdParams& P, const Hist& H, un
     fast_stamp(P, kTlLoss);
     return;
   }
-  // ---- loss.  The loss ticket is drawn as b's epilogue starts, so that its
-  // round trip overlaps the epilogue's loads; the block that draws the last
-  // one sums the loss.  Every other batch epilogue publishes its partial sum
+  if (P.B == 2) {
+    // ---- loss of two batch indices: each epilogue block swaps its partial
+    // sum (flag bit 32 | float bits) into one word with a returning atomic
+    // exchange.  The block that swaps second receives the other's partial,
+    // writes the loss and clears the word; the first is done.  No ticket and
+    // no wait: one device-scope round trip after the later epilogue.
+    const float total = epilogue<SOFT, MOM>(P, hist, repl, CK, CL, b, 1);
+    fast_stamp(P, kTlEpiEnd);
+    if (P.red == kRedNone || tid != 0) return;
+    for (int n = 0; n < P.publish_delay; ++n) __builtin_amdgcn_s_sleep(2);
+    const unsigned long long w =
+        xchg_dev(&P.part[0], (1ull << 32) | (unsigned long long)__float_as_uint(total));
+    if (w >> 32) {
+      store_dev(&P.part[0], 0ull);
+      // the bits of wave_sum over the two partials and zero lanes: their sum
+      // (either order), plus zero
+      const float sum = (total + __uint_as_float((unsigned)w)) + 0.0f;
+      P.loss[0] = P.red == kRedMean ? sum / (float)rows : sum;
+      fast_stamp(P, kTlLoss);
+    }
+    return;
+  }
+  // ---- loss of three or more batch indices.  The loss ticket is drawn as
+  // b's epilogue starts, so that its round trip overlaps the epilogue's
+  // loads; the block that draws the last one sums the loss.  Every other batch epilogue publishes its partial sum
   // as one word (flag bit 32 | float bits) -- no wait for its own writes, no
   // second ticket -- and the last block polls those words.  The blocks it
   // waits for drew their tickets earlier and run epilogues that wait on

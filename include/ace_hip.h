@@ -290,10 +290,11 @@ int ace_set_timeline(void* stamps);
  * forward's cross-block failure handling from the host, with every kernel
  * still exiting normally.  Process-wide, read by each later forward call.
  * max_polls bounds the loss block's wait for another batch index's partial
- * loss word (default 2^20 polls; 0 gives up at once wherever the word has
- * not arrived, and that loss is then NaN); publish_delay makes each batch
- * epilogue sleep about 128 * publish_delay cycles (s_sleep 2 each) before it publishes its
- * word (default 0).  A negative value restores the default.  Returns
+ * loss word when B > 2 (default 2^20 polls; 0 gives up at once wherever the
+ * word has not arrived, and that loss is then NaN; at B = 2 the two partials
+ * meet in one atomic exchange and nothing waits); publish_delay makes each
+ * batch epilogue sleep about 128 * publish_delay cycles (s_sleep 2 each)
+ * before it publishes its word (default 0).  A negative value restores the default.  Returns
  * ACE_EINVAL for max_polls > 2^20 or publish_delay > 2^16, else ACE_OK.
  */
 int ace_set_test_hooks(int max_polls, int publish_delay);

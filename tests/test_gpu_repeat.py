@@ -3,9 +3,9 @@ protocol (final-sum atomics, ticket counters reset by the block that draws
 the last ticket, loss partial words published and polled) must leave the
 workspace zero for the next launch, so repeated launches give bit-identical
 results and the workspace is all zero afterwards.  Covers the benchmark shape
-(one epilogue per batch index, loss polled from B = 2 partial words), a
-single batch index (one epilogue for everything) and B = 65 (partial words
-polled in two chunks), hard and soft."""
+(one epilogue per batch index, B = 2: the two partials meet in one word by an
+atomic exchange), a single batch index (one epilogue for everything) and
+B = 65 (partial words polled in two chunks), hard and soft."""
 
 from __future__ import annotations
 
