@@ -141,7 +141,7 @@ def assert_grad_close(grad: torch.Tensor, grad_ref: torch.Tensor, x: torch.Tenso
 
 def assert_lowp_grad_close(grad: torch.Tensor, grad_ref: torch.Tensor, x: torch.Tensor,
                            config: ACEConfig, atol: float = GRAD_ATOL,
-                           truth: torch.Tensor = None) -> torch.Tensor:
+                           truth: torch.Tensor = None, own: torch.Tensor = None) -> torch.Tensor:
     """dx in bfloat16 / float16 (the logits' type): every element within one
     unit in the last place of the reference's float32 gradient rounded to
     that type, plus the north star's atol -- both sides round a float32 value
@@ -151,8 +151,12 @@ def assert_lowp_grad_close(grad: torch.Tensor, grad_ref: torch.Tensor, x: torch.
     voxels whose probability is within 1e-6 of a bin boundary, and those
     rare (the rule of ``assert_grad_close``).  With ``truth`` (the float64
     gradient) an element also passes when it is at least as close to the
-    truth, rounded to the same type, as the reference is.  Returns the
-    [B, N] mask of voxels that do not pass."""
+    truth, rounded to the same type, as the reference is.  With ``own`` (the
+    float64 gradient at the kernels' own float32 probabilities) an element
+    also passes within one unit of it rounded to the same type: in bins of a
+    few soft voxels the gradient follows the probabilities' last bit, where
+    the kernels' correctly rounded softmax and torch's may differ by an ulp.
+    Returns the [B, N] mask of voxels that do not pass."""
     dt = grad.dtype
     assert dt in (torch.bfloat16, torch.float16), dt
     mant = 7 if dt == torch.bfloat16 else 10
@@ -164,6 +168,10 @@ def assert_lowp_grad_close(grad: torch.Tensor, grad_ref: torch.Tensor, x: torch.
     if truth is not None:
         t = truth.detach().cpu().double().to(dt).double().flatten(2)
         ok |= (g.double() - t).abs() <= (r.double() - t).abs()
+    if own is not None:
+        o = own.detach().cpu().double().to(dt).double().flatten(2)
+        eo = torch.floor(torch.log2(torch.clamp(o.abs(), min=torch.finfo(dt).tiny)))
+        ok |= (g.double() - o).abs() <= torch.exp2(eo - mant) + atol
     bad = (~ok).any(1)
     if bad.any():
         near = near_boundary_voxels(x, config)

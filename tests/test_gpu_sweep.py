@@ -21,7 +21,8 @@ import pytest
 import torch
 
 from ace_kernels import ACEConfig
-from gpu_helpers import LOSS_ATOL, LOSS_RTOL, assert_grad_close, assert_lowp_grad_close, run, say, truth64
+from gpu_helpers import (LOSS_ATOL, LOSS_RTOL, assert_grad_close, assert_lowp_grad_close, kernel_probs, run, say,
+                         truth64)
 
 pytestmark = pytest.mark.gpu
 
@@ -91,3 +92,36 @@ def test_sweep(i, b, c, spatial, dtype, kw) -> None:
         assert_grad_close(grad, grad_ref, x, cfg, rtol=1e-3, truth=grad64)
     else:
         assert_grad_close(grad, grad_ref, x, cfg)
+
+
+# 16-bit soft cases with a few voxels per bin from a 16 000-case soak of this
+# option space (new draw seeds, input seeds as below) whose one-element
+# gradient miss the rule above does not cover: one float16 unit beyond the
+# reference and the rounded float64 truth, within one unit of the float64
+# gradient at the kernels' own probabilities.
+RECORDED_LOWP = [
+    (1200107642, 3, 7, (16,), torch.float16,
+     dict(binning="soft", num_bins=33, activation="sigmoid", to_onehot_y=False, include_background=True,
+          ignore_empty_classes=False, reduction="mean", right=False)),
+    (1200208462, 1, 33, (3, 11, 15), torch.float16,
+     dict(binning="soft", num_bins=64, activation="softmax", to_onehot_y=False, include_background=True,
+          ignore_empty_classes=False, reduction="sum", right=True)),
+]
+
+
+@pytest.mark.parametrize("seed,b,c,spatial,dtype,kw", RECORDED_LOWP)
+def test_recorded_lowp_few_voxels(seed, b, c, spatial, dtype, kw) -> None:
+    from oracle.reference import register_reference
+    from test_gpu_soft_few_voxels import _at64
+
+    register_reference()
+    cfg = ACEConfig(**kw)
+    x, y = _inputs(seed, b, c, spatial, dtype, cfg)
+    say(f"recorded 16-bit few-voxel case: seed {seed} B={b} C={c} {spatial} {dtype} {kw}")
+    loss, grad = run("hip_mi355x", x.cuda(), y.cuda(), cfg)
+    loss_ref, grad_ref = run("reference", x.float(), y, cfg)
+    torch.testing.assert_close(loss.cpu(), loss_ref, rtol=LOSS_RTOL, atol=LOSS_ATOL)
+    _, grad64 = truth64(x, y, cfg)
+    _, own = _at64(kernel_probs(x, cfg), y, cfg)
+    assert_lowp_grad_close(grad, grad_ref, x, cfg, truth=grad64, own=own)
+
